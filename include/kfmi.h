@@ -1,0 +1,130 @@
+/*
+ * kfmi.h -- C ABI of the MI355X (gfx950) RoPE-aware attention prologue.
+ *
+ * The drop-in boundary for KernelFuser's attention-prologue path
+ * (WenbinWang12/KernelFuser).  The reference has no native boundary: its
+ * Python launchers start Triton kernels on torch's current stream.  Each entry
+ * point below replaces one of those launchers and names the reference
+ * function (file:line) whose launch it takes over.  References:
+ *   rope = src/e1_rope_publication_v1.py, qk = src/e1_qk_publication_v3.py.
+ *
+ * Conventions (all entry points):
+ *   - BF16 tensors are passed as raw device pointers to contiguous row-major
+ *     data in the reference layout: Q/out [B,Hq,S,D], K/V/KN [B,Hkv,S,D],
+ *     gamma [D], rotary tables [S,D] (split-half, duplicated halves), INV
+ *     float32 [B,Hq,S].  Pointers must be 16-byte aligned.
+ *   - D is 128 or 256; Hq % Hkv == 0; every tensor has < 2^31 elements
+ *     (rope:708-717).
+ *   - The caller owns every buffer.  No entry point allocates, frees or
+ *     synchronises; all work is enqueued on `stream` (a hipStream_t, NULL =
+ *     the legacy default stream), so calls are graph-capturable.
+ *   - Return value: KFMI_OK, or an error code with a message available from
+ *     kfmi_last_error() (thread-local).  Argument errors are detected before
+ *     any launch, so a failing call enqueues nothing.
+ */
+#ifndef KFMI_H
+#define KFMI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KFMI_ABI_VERSION 1
+
+/* status codes */
+#define KFMI_OK 0
+#define KFMI_EINVAL 1  /* invalid argument (shape, pointer, mode) */
+#define KFMI_ELAUNCH 2 /* HIP launch or runtime error */
+#define KFMI_EDEVICE 3 /* current device is not gfx950 */
+
+/* norm_style (rope:680-681, :697-698, :559-563); FP32 = single final rounding,
+ * the FP32 semantics of rope:119-130 (transform_debug). */
+#define KFMI_NORM_HF 0
+#define KFMI_NORM_LEGACY 1
+#define KFMI_NORM_FP32 2
+
+/* flags of kfmi_prepare_bf16 */
+#define KFMI_PREP_ONLY_K 1 /* rope:591-595 ONLY_K */
+#define KFMI_PREP_ROPE 2   /* rope:564 ROPE */
+
+/* mode of kfmi_launch_attention_bf16 (rope:668) */
+#define KFMI_MODE_QUERY 0   /* K prepared once, Q norm(+RoPE) in the attention prologue */
+#define KFMI_MODE_UNFUSED 1 /* Q and K prepared, plain attention */
+
+/* Version of this ABI (KFMI_ABI_VERSION). */
+int kfmi_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *kfmi_last_error(void);
+
+/* Row preparation: per-(token,head) RMSNorm(eps) * gamma, then optional
+ * rotate-half RoPE, BF16 out.  Replaces prepare_attention -> prepare_kernel
+ * (rope:652-658, :585-605, row math :550-582).  Q rows are skipped when
+ * flags has KFMI_PREP_ONLY_K (q and qn may then be NULL); cos/sin are read
+ * only when flags has KFMI_PREP_ROPE.  Also serves the isolated Q/K norm+RoPE
+ * workload (Q and K rows in one launch). */
+int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk,
+                      const void *cos, const void *sin, void *qn, void *kn,
+                      int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                      float eps, int norm_style, int flags, void *stream);
+
+/* Causal/non-causal GQA flash-attention prefill on bf16 MFMA.  Replaces the
+ * attention_v2_kernel launch (rope:674-677, kernel :608-649).
+ *   fuse_q = 1: q is raw; its RMSNorm (gq, eps, norm_style) and, when cos/sin
+ *               are non-NULL, RoPE run in the kernel prologue (FUSE_Q=True).
+ *   fuse_q = 0: q is already prepared (FUSE_Q=False).
+ * k must be prepared (KN).  scale multiplies q.k (the reference uses D^-1/2,
+ * rope:676).  bm is the number of query rows per workgroup (multiple of 32;
+ * 128 is the tuned value), bn the key tile (64 or 128; a scheduling hint,
+ * results do not depend on it). */
+int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *gq,
+                        const void *cos, const void *sin, void *out,
+                        int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                        double scale, float eps, int causal, int fuse_q, int norm_style,
+                        int bm, int bn, void *stream);
+
+/* Both launches of launch_attention (rope:661-677): mode QUERY prepares K
+ * into kn (K rows only) then runs attention with the fused Q prologue; mode
+ * UNFUSED prepares Q into qn and K into kn, then runs plain attention.  gk is
+ * K's gamma.  Scratch kn (and qn for UNFUSED) is caller-allocated, as the
+ * reference requires (rope:665-672).  cos/sin NULL disables RoPE. */
+int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
+                               const void *gq, const void *gk, const void *cos,
+                               const void *sin, void *out, void *qn, void *kn,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                               double scale, float eps, int causal, int mode,
+                               int norm_style, int bm, int bn, void *stream);
+
+/* Factored no-RoPE preparation (qk:592-609): INV[B,Hq,S] = rsqrt(mean q^2 +
+ * eps) (float32) for every Q row and KN = bf16(k * inv_k * gk * gq) for every
+ * K row (one rounding). */
+int kfmi_factored_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk,
+                               float *inv, void *kn, int64_t B, int64_t Hq, int64_t Hkv,
+                               int64_t S, int64_t D, float eps, void *stream);
+
+/* Factored attention (qk:612-638): scores = (q_raw . kn) * inv[row] * D^-1/2
+ * with exp2 online softmax; q is the RAW (un-normalised) BF16 query.
+ * inv_mode = 0: read inv (written by kfmi_factored_prepare_bf16);
+ * inv_mode = 1: compute each row's inverse RMS from q in the prologue
+ * (eps) and also write it to inv (which may then be NULL to skip the write). */
+int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, float *inv,
+                                 void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                                 int64_t D, float eps, int causal, int inv_mode, int bm, int bn,
+                                 void *stream);
+
+/* Both launches of launch_factored_attention (qk:641-652): KN preparation
+ * for the K rows, then factored attention that computes INV in its prologue
+ * and writes it to inv.  Outputs out, inv and kn match the reference's. */
+int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void *v,
+                                        const void *gq, const void *gk, void *out, float *inv,
+                                        void *kn, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                                        int64_t D, float eps, int causal, int bm, int bn,
+                                        void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KFMI_H */

@@ -1,0 +1,95 @@
+"""ctypes binding of the gfx950 C-ABI library (``include/kfmi.h``).
+
+The library is built in-tree by ``python -m kernelfuser_amd.build``.  There is
+no fallback: if the library is missing or cannot be loaded, every op raises.
+torch is imported first so the HIP runtime torch ships is the one the library
+binds to (both use the ``libamdhip64.so.7`` soname).
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime before the library)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
+ABI_VERSION = 1
+
+KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
+NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
+PREP_ONLY_K, PREP_ROPE = 1, 2
+MODE_QUERY, MODE_UNFUSED = 0, 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+_F = ctypes.c_float
+_D = ctypes.c_double
+
+# name -> argtypes (restype is int for all compute entry points)
+SIGNATURES = {
+    "kfmi_prepare_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
+    "kfmi_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D, _F, _I, _I, _I, _I, _I, _P],
+    "kfmi_launch_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D, _F,
+                                   _I, _I, _I, _I, _I, _P],
+    "kfmi_factored_prepare_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
+    "kfmi_factored_attention_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P],
+    "kfmi_launch_factored_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I,
+                                            _I, _I, _P],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class KfmiError(RuntimeError):
+    """A non-argument failure reported by the native library."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the native library; raises if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"kfmi native library not found at {LIB_PATH}; build it with "
+                "`python -m kernelfuser_amd.build` (there is no CPU fallback)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        lib.kfmi_abi_version.restype = ctypes.c_int
+        lib.kfmi_abi_version.argtypes = []
+        lib.kfmi_last_error.restype = ctypes.c_char_p
+        lib.kfmi_last_error.argtypes = []
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        if lib.kfmi_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"kfmi ABI version {lib.kfmi_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call a compute entry point; map its status to ValueError / KfmiError."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc == KFMI_OK:
+        return
+    msg = lib.kfmi_last_error().decode(errors="replace")
+    if rc == KFMI_EINVAL:
+        raise ValueError(f"{name}: {msg}")
+    raise KfmiError(f"{name} failed (status {rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Raw hipStream_t of torch's current stream on ``t``'s device."""
+    return torch.cuda.current_stream(t.device).cuda_stream

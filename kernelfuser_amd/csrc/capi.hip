@@ -1,0 +1,233 @@
+// C ABI of the gfx950 attention-prologue library (declared in include/kfmi.h).
+// Validates every argument before enqueuing anything, then dispatches to the
+// kernel launchers.  No allocation, no synchronisation.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "kfmi.h"
+#include "kfmi_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int launch_status(hipError_t e, const char *what) {
+  if (e != hipSuccess) return fail(KFMI_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  g_error.clear();
+  return KFMI_OK;
+}
+
+// gfx950 check of the current device, cached per device ordinal.
+int check_device() {
+  static std::mutex mu;
+  static int cached[64];  // 0 unknown, 1 ok, 2 wrong arch
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(KFMI_EDEVICE, "hipGetDevice failed");
+  if (dev < 0 || dev >= 64) return fail(KFMI_EDEVICE, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (cached[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(KFMI_EDEVICE, "hipGetDeviceProperties failed");
+    cached[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    if (cached[dev] == 2) return fail(KFMI_EDEVICE, "device %d is %s; this library is built for gfx950", dev, prop.gcnArchName);
+  }
+  if (cached[dev] == 2) return fail(KFMI_EDEVICE, "device %d is not gfx950", dev);
+  return KFMI_OK;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shape rules shared by all entry points (rope:705-717).
+int check_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D) {
+  if (B < 1 || Hq < 1 || Hkv < 1 || S < 1) return fail(KFMI_EINVAL, "B, Hq, Hkv and S must be >= 1 (got %lld, %lld, %lld, %lld)",
+                                                      (long long)B, (long long)Hq, (long long)Hkv, (long long)S);
+  if (D != 128 && D != 256) return fail(KFMI_EINVAL, "D must be 128 or 256 (got %lld)", (long long)D);
+  if (Hq % Hkv != 0) return fail(KFMI_EINVAL, "Hq (%lld) must be a multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  const int64_t lim = (int64_t)1 << 31;
+  if (B * Hq * S * D >= lim || B * Hkv * S * D >= lim) return fail(KFMI_EINVAL, "tensors must have fewer than 2^31 elements");
+  return KFMI_OK;
+}
+
+int check_ptrs(std::initializer_list<std::pair<const void *, const char *>> ptrs) {
+  for (auto &pr : ptrs) {
+    if (pr.first == nullptr) return fail(KFMI_EINVAL, "%s must not be NULL", pr.second);
+    if (!aligned16(pr.first)) return fail(KFMI_EINVAL, "%s must be 16-byte aligned", pr.second);
+  }
+  return KFMI_OK;
+}
+
+int check_style(int norm_style) {
+  if (norm_style != KFMI_NORM_HF && norm_style != KFMI_NORM_LEGACY && norm_style != KFMI_NORM_FP32)
+    return fail(KFMI_EINVAL, "norm_style must be KFMI_NORM_HF, KFMI_NORM_LEGACY or KFMI_NORM_FP32 (got %d)", norm_style);
+  return KFMI_OK;
+}
+
+int check_tiles(int bm, int bn) {
+  if (bm < 32 || bm > 256 || bm % 32 != 0) return fail(KFMI_EINVAL, "bm must be a multiple of 32 in [32, 256] (got %d)", bm);
+  if (bn != 32 && bn != 64 && bn != 128) return fail(KFMI_EINVAL, "bn must be 32, 64 or 128 (got %d)", bn);
+  return KFMI_OK;
+}
+
+int style_of(int norm_style) {
+  return norm_style == KFMI_NORM_HF ? kfmi::ST_HF : norm_style == KFMI_NORM_LEGACY ? kfmi::ST_LEGACY : kfmi::ST_FP32;
+}
+
+#define KFMI_TRY(x)            \
+  do {                         \
+    int rc_ = (x);             \
+    if (rc_ != KFMI_OK) return rc_; \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int kfmi_abi_version(void) { return KFMI_ABI_VERSION; }
+
+const char *kfmi_last_error(void) { return g_error.c_str(); }
+
+int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk, const void *cos,
+                      const void *sin, void *qn, void *kn, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                      int64_t D, float eps, int norm_style, int flags, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_style(norm_style));
+  if (flags & ~(KFMI_PREP_ONLY_K | KFMI_PREP_ROPE)) return fail(KFMI_EINVAL, "unknown flags 0x%x", flags);
+  const bool only_k = flags & KFMI_PREP_ONLY_K, rope = flags & KFMI_PREP_ROPE;
+  KFMI_TRY(check_ptrs({{k, "k"}, {gk, "gk"}, {kn, "kn"}}));
+  if (!only_k) KFMI_TRY(check_ptrs({{q, "q"}, {gq, "gq"}, {qn, "qn"}}));
+  if (rope) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
+  if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
+  KFMI_TRY(check_device());
+  kfmi::RowsArgs a{};
+  a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.gq = (const uint16_t *)gq; a.gk = (const uint16_t *)gk;
+  a.cos = (const uint16_t *)cos; a.sin = (const uint16_t *)sin;
+  a.qn = (uint16_t *)qn; a.kn = (uint16_t *)kn; a.inv = nullptr;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
+  a.only_k = only_k; a.rope = rope; a.style = style_of(norm_style); a.eps = eps;
+  return launch_status(kfmi::launch_rows(a, (hipStream_t)stream), "prepare launch");
+}
+
+static int attention_impl(const void *q, const void *k, const void *v, const void *gq, const void *cos,
+                          const void *sin, void *out, float *inv, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+                          int64_t D, double scale, float eps, int causal, int prologue, int style, int bm, int bn,
+                          hipStream_t stream) {
+  kfmi::AttnArgs a{};
+  a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.v = (const uint16_t *)v; a.gq = (const uint16_t *)gq;
+  a.cos = (const uint16_t *)cos; a.sin = (const uint16_t *)sin; a.out = (uint16_t *)out; a.inv = inv;
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
+  a.causal = causal != 0; a.prologue = prologue; a.style = style; a.scale = scale; a.eps = eps;
+  a.bm = bm; a.bn = bn;
+  return launch_status(kfmi::launch_attention(a, stream), "attention launch");
+}
+
+int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *cos, const void *sin,
+                        void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps,
+                        int causal, int fuse_q, int norm_style, int bm, int bn, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_style(norm_style));
+  KFMI_TRY(check_tiles(bm, bn));
+  KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {out, "out"}}));
+  if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
+  if (fuse_q) KFMI_TRY(check_ptrs({{gq, "gq"}}));
+  if (fuse_q && cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
+  if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
+  KFMI_TRY(check_device());
+  const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
+  return attention_impl(q, k, v, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
+                        style_of(norm_style), bm, bn, (hipStream_t)stream);
+}
+
+int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                               const void *cos, const void *sin, void *out, void *qn, void *kn, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal,
+                               int mode, int norm_style, int bm, int bn, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_style(norm_style));
+  KFMI_TRY(check_tiles(bm, bn));
+  if (mode != KFMI_MODE_QUERY && mode != KFMI_MODE_UNFUSED) return fail(KFMI_EINVAL, "Invalid fusion mode %d", mode);
+  KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}}));
+  if (kn == nullptr || (mode == KFMI_MODE_UNFUSED && qn == nullptr)) return fail(KFMI_EINVAL, "Missing scratch buffers");
+  KFMI_TRY(check_ptrs({{kn, "kn"}}));
+  if (mode == KFMI_MODE_UNFUSED) KFMI_TRY(check_ptrs({{qn, "qn"}}));
+  if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
+  if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
+  if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
+  KFMI_TRY(check_device());
+  const bool rope = cos != nullptr;
+  kfmi::RowsArgs r{};
+  r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
+  r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;
+  r.B = B; r.Hq = Hq; r.Hkv = Hkv; r.S = S; r.D = D;
+  r.only_k = mode == KFMI_MODE_QUERY; r.rope = rope; r.style = style_of(norm_style); r.eps = eps;
+  hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
+  if (e != hipSuccess) return launch_status(e, "prepare launch");
+  const bool query = mode == KFMI_MODE_QUERY;
+  const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
+  return attention_impl(query ? q : qn, kn, v, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
+                        style_of(norm_style), bm, bn, (hipStream_t)stream);
+}
+
+int kfmi_factored_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk, float *inv, void *kn,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, float eps, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {gq, "gq"}, {gk, "gk"}, {inv, "inv"}, {kn, "kn"}}));
+  if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
+  KFMI_TRY(check_device());
+  kfmi::RowsArgs r{};
+  r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
+  r.kn = (uint16_t *)kn; r.inv = inv;
+  r.B = B; r.Hq = Hq; r.Hkv = Hkv; r.S = S; r.D = D;
+  r.only_k = false; r.rope = false; r.style = kfmi::ST_FACTORED; r.eps = eps;
+  return launch_status(kfmi::launch_rows(r, (hipStream_t)stream), "factored prepare launch");
+}
+
+int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, float *inv, void *out, int64_t B,
+                                 int64_t Hq, int64_t Hkv, int64_t S, int64_t D, float eps, int causal, int inv_mode,
+                                 int bm, int bn, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_tiles(bm, bn));
+  KFMI_TRY(check_ptrs({{q, "q"}, {kn, "kn"}, {v, "v"}, {out, "out"}}));
+  if (inv_mode != 0 && inv_mode != 1) return fail(KFMI_EINVAL, "inv_mode must be 0 (read) or 1 (compute)");
+  if (inv_mode == 0) KFMI_TRY(check_ptrs({{inv, "inv"}}));
+  if (inv && (reinterpret_cast<uintptr_t>(inv) & 3u)) return fail(KFMI_EINVAL, "inv must be 4-byte aligned");
+  KFMI_TRY(check_device());
+  const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
+                        kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
+}
+
+int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                                        void *out, float *inv, void *kn, int64_t B, int64_t Hq, int64_t Hkv,
+                                        int64_t S, int64_t D, float eps, int causal, int bm, int bn, void *stream) {
+  KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
+  KFMI_TRY(check_tiles(bm, bn));
+  KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}, {inv, "inv"}, {kn, "kn"}}));
+  if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
+  KFMI_TRY(check_device());
+  kfmi::RowsArgs r{};
+  r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
+  r.kn = (uint16_t *)kn; r.inv = inv;
+  r.B = B; r.Hq = Hq; r.Hkv = Hkv; r.S = S; r.D = D;
+  r.only_k = true; r.rope = false; r.style = kfmi::ST_FACTORED; r.eps = eps;
+  hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
+  if (e != hipSuccess) return launch_status(e, "factored prepare launch");
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
+                        kfmi::PRO_FACTORED_CALC, kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Host-side launch descriptors shared by the C ABI and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kfmi {
+
+// Row styles of the preparation and attention-prologue arithmetic.
+enum Style : int {
+  ST_HF = 0,       // BF16 at each HF op boundary (norm, x gamma, each RoPE product, +/-)
+  ST_LEGACY = 1,   // one BF16 cast of x*inv*gamma, then the BF16 RoPE chain
+  ST_FP32 = 2,     // FP32 throughout, one final BF16 rounding
+  ST_FACTORED = 3  // Q rows -> FP32 inverse RMS; K rows -> bf16(k*inv*gk*gq)
+};
+
+// Attention prologue kinds.
+enum Prologue : int {
+  PRO_NONE = 0,          // Q already prepared
+  PRO_NORM = 1,          // Q RMSNorm in the prologue
+  PRO_NORM_ROPE = 2,     // Q RMSNorm + rotate-half RoPE in the prologue
+  PRO_FACTORED_READ = 3, // raw Q, per-row inverse RMS read from inv[]
+  PRO_FACTORED_CALC = 4  // raw Q, per-row inverse RMS computed (and written to inv[])
+};
+
+struct RowsArgs {
+  const uint16_t *q, *k, *gq, *gk, *cos, *sin;
+  uint16_t *qn, *kn;
+  float *inv;
+  int64_t B, Hq, Hkv, S, D;
+  bool only_k, rope;
+  int style;
+  float eps;
+};
+
+struct AttnArgs {
+  const uint16_t *q, *k, *v, *gq, *cos, *sin;
+  uint16_t *out;
+  float *inv;
+  int64_t B, Hq, Hkv, S, D;
+  bool causal;
+  int prologue, style;
+  double scale;  // multiplies q.k (ignored by the factored prologues: D^-1/2)
+  float eps;
+  int bm, bn;
+};
+
+// Both return hipSuccess or the launch error.  Arguments are validated by the caller.
+hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
+hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
+
+}  // namespace kfmi

@@ -1,0 +1,214 @@
+// Row preparation kernels for gfx950: per-(token, head) RMSNorm * gamma with
+// optional rotate-half RoPE (the reference's prepare_kernel/_rows,
+// src/e1_rope_publication_v1.py:550-605) and the factored no-RoPE
+// preparation (src/e1_qk_publication_v3.py:592-609).
+//
+// Memory-bound design:
+//  * a D-wide BF16 row is D/8 lanes x 16 bytes (one 16-lane DPP row for D=128),
+//    so a wave64 covers 64/(D/8) consecutive positions of one head and its
+//    loads/stores are single contiguous runs of 1 KiB;
+//  * the sum of squares is reduced with DPP inside the row, the rotate-half
+//    partner (column d +/- D/2) is the lane D/16 away (row_ror:8 for D=128);
+//  * a wave keeps the cos/sin rows of its positions and both gamma vectors in
+//    registers and walks a chunk of heads, so tables are read once per
+//    position per head chunk, not once per row;
+//  * FP32 internal arithmetic; the rounding points follow the selected style.
+#include "kfmi_device.h"
+#include "kfmi_launch.h"
+
+namespace kfmi {
+namespace {
+
+struct RowsParams {
+  const uint16_t *q, *k, *gq, *gk, *cos, *sin;
+  uint16_t *qn, *kn;
+  float *inv;
+  int64_t S;
+  int B, Hq_rows, Hq, Hkv;  // Hq_rows = Q heads processed (0 = K rows only); Hq = Q tensor heads
+  int heads_per_chunk, n_groups;
+  float eps;
+};
+
+// Normalised element x*inv*gamma with the rounding points of a style.
+template <int ST>
+__device__ __forceinline__ float norm_elem(float x, float inv, float g) {
+  if (ST == ST_HF) return round_bf16(round_bf16(x * inv) * g);  // rope:560-561
+  if (ST == ST_LEGACY) return round_bf16(__fmul_rn(__fmul_rn(x, inv), g));  // rope:563
+  return __fmul_rn(__fmul_rn(x, inv), g);  // FP32: rope:125, rope:298
+}
+
+// rotate-half output of one element: first half n*c - np*s, second half n*c + np*s.
+template <int ST>
+__device__ __forceinline__ float rope_elem(float n, float np, float c, float s, bool first) {
+  if (ST == ST_FP32) {  // rope:129 / rope:164-167 (fp32=True): two products, one add
+    float p0 = __fmul_rn(n, c), p1 = __fmul_rn(np, s);
+    return first ? __fsub_rn(p0, p1) : __fadd_rn(p0, p1);
+  }
+  float p0 = round_bf16(n * c), p1 = round_bf16(np * s);  // rope:578-579
+  return first ? p0 - p1 : p0 + p1;  // rounded to BF16 at the store (rope:580-581)
+}
+
+// Raw 16-byte chunk held by the rotate-half partner lane (lane ^ LPR/2).
+template <int LPR>
+__device__ __forceinline__ u32x4_t partner_chunk(const u32x4_t &x) {
+  u32x4_t r;
+  if constexpr (LPR == 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = dpp_u32<DPP_ROW_ROR8>(x[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (uint32_t)__shfl_xor((int)x[i], LPR / 2);
+  }
+  return r;
+}
+
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  x = sum16(x);
+  if constexpr (LPR == 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+template <int D, int ST, bool ROPE, bool ONLY_K>
+__global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
+  constexpr int LPR = D / 8;     // lanes per row
+  constexpr int RPW = 64 / LPR;  // positions per wave
+  constexpr int HALF = LPR / 2;
+  constexpr int U = 4;           // heads in flight per lane
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wave >= p.B * p.n_groups) return;  // wave-uniform
+  const int b = wave / p.n_groups;
+  const int64_t pos = (int64_t)(wave % p.n_groups) * RPW + lane / LPR;
+  const int lc = lane % LPR;
+  const int d0 = lc * 8;
+  const int dp = (lc ^ HALF) * 8;  // column of the partner chunk
+  const bool valid = pos < p.S;
+  const bool first = lc < HALF;
+  const int Hq_rows = ONLY_K ? 0 : p.Hq_rows;
+  const int H = Hq_rows + p.Hkv;
+  const int h_begin = blockIdx.y * p.heads_per_chunk;
+  const int h_end = min(H, h_begin + p.heads_per_chunk);
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+
+  float cs[8], sn[8];
+  if (ROPE) {
+    unpack8(valid ? ld16(p.cos + pos * D + d0) : zero, cs);
+    unpack8(valid ? ld16(p.sin + pos * D + d0) : zero, sn);
+  }
+  const u32x4_t gq_own = Hq_rows ? ld16(p.gq + d0) : zero;
+  const u32x4_t gq_par = (Hq_rows && ROPE) ? ld16(p.gq + dp) : zero;
+  const u32x4_t gk_own = ld16(p.gk + d0);
+  const u32x4_t gk_par = ROPE ? ld16(p.gk + dp) : zero;
+  const u32x4_t gq_fac = (ST == ST_FACTORED) ? ld16(p.gq + d0) : zero;
+
+  for (int h0 = h_begin; h0 < h_end; h0 += U) {
+    u32x4_t xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int hh = h0 + u;
+      const uint16_t *src = hh < Hq_rows
+                                ? p.q + (((int64_t)b * p.Hq + hh) * p.S + pos) * D + d0
+                                : p.k + (((int64_t)b * p.Hkv + (hh - Hq_rows)) * p.S + pos) * D + d0;
+      xv[u] = (hh < h_end && valid) ? ld16(src) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int hh = h0 + u;
+      if (hh >= h_end) break;  // wave-uniform
+      const bool is_q = hh < Hq_rows;
+      float x[8];
+      unpack8(xv[u], x);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
+      ss = row_sum<LPR>(ss);
+      const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+      const int64_t row = is_q ? ((int64_t)b * p.Hq + hh) * p.S + pos
+                               : ((int64_t)b * p.Hkv + (hh - Hq_rows)) * p.S + pos;
+      if constexpr (ST == ST_FACTORED) {
+        if (is_q) {  // qk:597-601: FP32 inverse RMS per Q row
+          if (valid && lc == 0) p.inv[row] = inv;
+        } else {     // qk:602-609: one rounding of x*inv*gk*gq
+          float gk[8], gq[8], y[8];
+          unpack8(gk_own, gk);
+          unpack8(gq_fac, gq);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), gk[j]), gq[j]);
+          if (valid) st16(p.kn + row * D + d0, pack8(y));
+        }
+      } else {
+        float go[8], y[8];
+        unpack8(is_q ? gq_own : gk_own, go);
+        if constexpr (ROPE) {
+          float xp[8], gp[8];
+          unpack8(partner_chunk<LPR>(xv[u]), xp);
+          unpack8(is_q ? gq_par : gk_par, gp);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float n = norm_elem<ST>(x[j], inv, go[j]);
+            const float np = norm_elem<ST>(xp[j], inv, gp[j]);
+            y[j] = rope_elem<ST>(n, np, cs[j], sn[j], first);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) y[j] = norm_elem<ST>(x[j], inv, go[j]);
+        }
+        uint16_t *dst = (is_q ? p.qn : p.kn) + row * D + d0;
+        if (valid) st16(dst, pack8(y));
+      }
+    }
+  }
+}
+
+template <int D, int ST, bool ROPE, bool ONLY_K>
+hipError_t launch_rows_t(const RowsParams &p, int blocks_x, int blocks_y, hipStream_t stream) {
+  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K>), dim3(blocks_x, blocks_y), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, int ST, bool ROPE>
+hipError_t dispatch_k(const RowsParams &p, int bx, int by, hipStream_t s) {
+  return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false>(p, bx, by, s) : launch_rows_t<D, ST, ROPE, true>(p, bx, by, s);
+}
+
+template <int D>
+hipError_t dispatch_rows(const RowsParams &p, int style, bool rope, int bx, int by, hipStream_t s) {
+  switch (style) {
+    case ST_HF: return rope ? dispatch_k<D, ST_HF, true>(p, bx, by, s) : dispatch_k<D, ST_HF, false>(p, bx, by, s);
+    case ST_LEGACY: return rope ? dispatch_k<D, ST_LEGACY, true>(p, bx, by, s) : dispatch_k<D, ST_LEGACY, false>(p, bx, by, s);
+    case ST_FP32: return rope ? dispatch_k<D, ST_FP32, true>(p, bx, by, s) : dispatch_k<D, ST_FP32, false>(p, bx, by, s);
+    case ST_FACTORED: return dispatch_k<D, ST_FACTORED, false>(p, bx, by, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
+  RowsParams p;
+  p.q = a.q; p.k = a.k; p.gq = a.gq; p.gk = a.gk; p.cos = a.cos; p.sin = a.sin;
+  p.qn = a.qn; p.kn = a.kn; p.inv = a.inv;
+  p.S = a.S;
+  p.B = (int)a.B;
+  p.Hq = (int)a.Hq;
+  p.Hq_rows = a.only_k ? 0 : (int)a.Hq;
+  p.Hkv = (int)a.Hkv;
+  p.eps = a.eps;
+  const int lpr = (int)a.D / 8;
+  const int rpw = 64 / lpr;
+  p.n_groups = (int)((a.S + rpw - 1) / rpw);
+  const int H = p.Hq_rows + p.Hkv;
+  // Split the heads into chunks so the grid holds >= 8192 waves (32 per CU)
+  // when the position count alone does not.
+  const int64_t waves = (int64_t)p.B * p.n_groups;
+  int chunks = (int)((8192 + waves - 1) / waves);
+  chunks = chunks < 1 ? 1 : (chunks > H ? H : chunks);
+  p.heads_per_chunk = (H + chunks - 1) / chunks;
+  const int by = (H + p.heads_per_chunk - 1) / p.heads_per_chunk;
+  const int bx = (int)((waves + 3) / 4);
+  if (a.D == 128) return dispatch_rows<128>(p, a.style, a.rope, bx, by, stream);
+  return dispatch_rows<256>(p, a.style, a.rope, bx, by, stream);
+}
+
+}  // namespace kfmi

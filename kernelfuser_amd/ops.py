@@ -1,0 +1,312 @@
+"""Reference-signature ops of the RoPE-aware attention prologue on gfx950.
+
+Each public function keeps the name, arguments, defaults and error behaviour of
+the reference function it replaces (WenbinWang12/KernelFuser; ``rope`` =
+src/e1_rope_publication_v1.py, ``qk`` = src/e1_qk_publication_v3.py) and runs
+the hand-written gfx950 HIP kernels through the C ABI (``include/kfmi.h``).
+There is no CPU or eager fallback: without the native library, or on another
+GPU architecture, every op raises.
+
+Differences from the reference, all deliberate:
+  * ``norm_style`` also accepts ``'fp32'``: FP32 RMSNorm*gamma and RoPE with one
+    final BF16 rounding (the FP32 semantics of rope:119-130).  ``'hf'`` stays the
+    default of ``optimized_attention`` as in the reference.
+  * The SM90 requirement (rope:718) becomes a gfx950 (MI355X) requirement.
+  * Triton tuning knobs (``rows``, ``warps``, ``stages``, ``gather``) are accepted
+    and ignored; ``bm``/``bn`` are tile hints -- results do not depend on them.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import MODE_QUERY, MODE_UNFUSED, NORM_STYLES, PREP_ONLY_K, PREP_ROPE, ptr, stream_of
+
+EPS = 1e-6  # rope:32; the reference kernels hard-code it (rope:558)
+
+# Attention geometries (Hq, Hkv, D) of the reference's model table (rope:18-24).
+MODELS = {
+    "Qwen3-0.6B": (16, 8, 128), "Qwen3-1.7B": (32, 8, 128),
+    "Qwen3-4B": (32, 8, 128), "Qwen3-8B": (32, 8, 128),
+    "Qwen3-32B": (64, 8, 128), "Qwen3-30B-A3B": (32, 4, 128),
+    "Gemma-3-4B": (8, 4, 256), "Gemma-3-12B": (16, 8, 256),
+    "Gemma-3-27B": (32, 16, 128),
+}
+
+_arch_cache: dict[int, str] = {}
+
+
+def device_arch(device: torch.device) -> str:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _arch_cache:
+        _arch_cache[idx] = torch.cuda.get_device_properties(idx).gcnArchName
+    return _arch_cache[idx]
+
+
+def _style(norm_style: Optional[str], hf_norm: bool) -> int:
+    style = norm_style if norm_style is not None else ("hf" if hf_norm else "legacy")
+    if style not in NORM_STYLES:
+        raise ValueError(f"norm_style must be one of {sorted(NORM_STYLES)}, got {style!r}")
+    return NORM_STYLES[style]
+
+
+# ---------------------------------------------------------------------------
+# Low-level launchers (caller-preallocated buffers, no checks beyond the C ABI's)
+# ---------------------------------------------------------------------------
+
+def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_norm=True, norm_style=None):
+    """RMSNorm*gamma (+ rotate-half RoPE) of K rows into ``kn`` and, unless
+    ``only_k``, of Q rows into ``qn`` in one launch (rope:652-658).
+
+    ``inputs`` is the reference 7-tuple ``(q, k, v, gq, gk, cos, sin)``; with
+    ``rope=False`` the table entries are ignored.  ``rows`` (Triton rows per
+    program) is ignored.
+    """
+    q, k, v, gq, gk, cos, sin = inputs
+    b, h, s, d = q.shape
+    flags = (PREP_ONLY_K if only_k else 0) | (PREP_ROPE if rope else 0)
+    _lib.call("kfmi_prepare_bf16",
+              None if only_k else ptr(q), ptr(k), None if only_k else ptr(gq), ptr(gk),
+              ptr(cos) if rope else None, ptr(sin) if rope else None,
+              None if only_k else ptr(qn), ptr(kn),
+              b, h, k.shape[1], s, d, EPS, _style(norm_style, hf_norm), flags, stream_of(k))
+
+
+def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, warps=4, stages=1,
+                     gather=True, rope=True, hf_norm=True, qn=None, kn=None, norm_style=None):
+    """Preparation + attention launches of the reference launcher (rope:661-677).
+
+    ``mode='query'``: K is prepared once into ``kn``; Q's norm (+RoPE) runs in the
+    attention prologue.  ``mode='unfused'``: Q into ``qn`` and K into ``kn``, then
+    plain attention.  Scratch buffers must be preallocated (rope:665-672).  Timings
+    must include both launches, as this function issues them.
+    """
+    if mode not in ("full", "query", "unfused"):
+        raise ValueError("Invalid fusion mode")
+    if mode == "full":
+        raise NotImplementedError(
+            "mode='full' (K norm+RoPE recomputed per key tile) is not provided by the gfx950 "
+            "library; use 'query' (K prepared once) or 'unfused'")
+    if kn is None or (mode == "unfused" and qn is None):
+        raise ValueError("Missing scratch buffers")
+    q, k, v, gq, gk, cos, sin = inputs
+    b, h, s, d = q.shape
+    _lib.call("kfmi_launch_attention_bf16",
+              ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk),
+              ptr(cos) if rope else None, ptr(sin) if rope else None,
+              ptr(out), ptr(qn), ptr(kn),
+              b, h, k.shape[1], s, d, float(d) ** -0.5, EPS, int(bool(causal)),
+              MODE_QUERY if mode == "query" else MODE_UNFUSED, _style(norm_style, hf_norm),
+              _bm(bm), _bn(bn), stream_of(q))
+
+
+def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=64):
+    """No-RoPE factored launch (qk:641-652): ``kn = bf16(k*inv_k*gk*gq)`` and FP32
+    ``inv`` ``[B,Hq,S]`` (Q's inverse RMS, applied to the scores) are written to the
+    caller's buffers, then factored attention writes ``out``.  ``inputs`` uses the
+    reference five-tensor order ``(q, k, v, gq, gk)``.
+    """
+    q, k, v, gq, gk = inputs[:5]
+    b, h, s, d = q.shape
+    _lib.call("kfmi_launch_factored_attention_bf16",
+              ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk), ptr(out), ptr(inv), ptr(kn),
+              b, h, k.shape[1], s, d, EPS, int(bool(causal)), _bm(bm), _bn(bn), stream_of(q))
+
+
+def prepare_factored(inputs, inv, kn):
+    """The factored preparation alone (qk:592-609): ``inv`` for every Q row and
+    ``kn`` for every K row, one launch."""
+    q, k, v, gq, gk = inputs[:5]
+    b, h, s, d = q.shape
+    _lib.call("kfmi_factored_prepare_bf16", ptr(q), ptr(k), ptr(gq), ptr(gk), ptr(inv), ptr(kn),
+              b, h, k.shape[1], s, d, EPS, stream_of(q))
+
+
+def factored_attention(q, kn, v, inv, out, *, causal=False, bm=64, bn=64, compute_inv=False):
+    """The factored attention launch alone (qk:612-638) on raw ``q`` and prepared
+    ``kn``; ``compute_inv=True`` derives Q's inverse RMS in the prologue (and
+    writes it to ``inv`` when given) instead of reading ``inv``."""
+    b, h, s, d = q.shape
+    _lib.call("kfmi_factored_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(inv), ptr(out),
+              b, h, kn.shape[1], s, d, EPS, int(bool(causal)), int(bool(compute_inv)), _bm(bm), _bn(bn),
+              stream_of(q))
+
+
+def _bm(bm):
+    return int(bm) if int(bm) % 32 == 0 and 32 <= int(bm) <= 256 else 128
+
+
+def _bn(bn):
+    return int(bn) if int(bn) in (32, 64, 128) else 64
+
+
+# ---------------------------------------------------------------------------
+# Validated, allocating API
+# ---------------------------------------------------------------------------
+
+def _check_device(tensors, device):
+    if any((not t.is_cuda) or t.device != device or t.dtype != torch.bfloat16 or not t.is_contiguous()
+           for t in tensors):
+        raise ValueError("Inputs must be contiguous BF16 tensors on one GPU device")
+    if not device_arch(device).startswith("gfx950"):
+        raise ValueError(f"This implementation targets gfx950 (MI355X); device is {device_arch(device)}")
+
+
+def optimized_attention(q, k, v, gq, gk, cos=None, sin=None, *, causal=False, mode="query", bn=128,
+                        gather=False, norm_style="hf"):
+    """Forward BF16 attention with Q/K RMSNorm (+ optional split-half RoPE) fused
+    into the prologue (rope:680-726).
+
+    ``mode='query'`` prepares K once and fuses Q's norm (and RoPE when both
+    tables are given) into the attention prologue; ``mode='unfused'`` prepares Q
+    and K, then runs the same attention.  ``norm_style``: ``'hf'`` rounds at HF's
+    BF16 op boundaries, ``'legacy'`` casts x*inv*gamma once, ``'fp32'`` keeps the
+    whole prologue in FP32 with one final rounding.  Forward only; projections,
+    KV caches and backward are out of scope.  Every argument error raises
+    ``ValueError`` before anything is launched (rope:695-719).
+    """
+    if mode not in ("query", "unfused") or bn not in (64, 128):
+        raise ValueError("mode must be 'query' or 'unfused' and bn must be 64 or 128")
+    if norm_style not in NORM_STYLES:
+        raise ValueError("norm_style must be 'hf', 'legacy' or 'fp32'")
+    if (cos is None) != (sin is None):
+        raise ValueError("Pass both rotary tables (cos and sin) or neither")
+    rotary = cos is not None
+    tensors = (q, k, v, gq, gk) + ((cos, sin) if rotary else ())
+    if any(t.requires_grad for t in tensors):
+        raise ValueError("optimized_attention is forward-only")
+    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
+        raise ValueError("Expected q [B,Hq,S,D] and k, v [B,Hkv,S,D]")
+    b, h, s, d = q.shape
+    if (d not in (128, 256) or min(b, h, s) < 1 or k.shape[0] != b or tuple(k.shape[2:]) != (s, d)
+            or k.shape[1] < 1 or h % k.shape[1]):
+        raise ValueError("Expected D in (128, 256), matching batch and sequence, and Hq a multiple of Hkv")
+    if (tuple(gq.shape) != (d,) or tuple(gk.shape) != (d,)
+            or (rotary and (tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d)))):
+        raise ValueError("Expected gamma vectors [D] and optional rotary tables [S,D]")
+    _check_device(tensors, q.device)
+    if max(q.numel(), k.numel()) >= 2 ** 31:
+        raise ValueError("Tensors must have fewer than 2**31 elements")
+    return torch.ops.kfmi.optimized_attention(q, k, v, gq, gk, cos, sin, bool(causal), mode, int(bn), norm_style)
+
+
+def norm_rope(q, k, gq, gk, cos=None, sin=None, *, norm_style="fp32", qn=None, kn=None):
+    """Isolated per-head Q/K RMSNorm (+ rotate-half RoPE): one launch over every Q
+    and K row (the ``only_k=False`` preparation of rope:652-658).  Returns
+    ``(qn, kn)``, allocating them unless given."""
+    if norm_style not in NORM_STYLES:
+        raise ValueError("norm_style must be 'hf', 'legacy' or 'fp32'")
+    if (cos is None) != (sin is None):
+        raise ValueError("Pass both rotary tables (cos and sin) or neither")
+    if q.ndim != 4 or k.ndim != 4 or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+        raise ValueError("Expected q [B,Hq,S,D] and k [B,Hkv,S,D]")
+    b, h, s, d = q.shape
+    if d not in (128, 256) or h % k.shape[1]:
+        raise ValueError("Expected D in (128, 256) and Hq a multiple of Hkv")
+    if tuple(gq.shape) != (d,) or tuple(gk.shape) != (d,) or (cos is not None and (
+            tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d))):
+        raise ValueError("Expected gamma vectors [D] and optional rotary tables [S,D]")
+    tensors = (q, k, gq, gk) + ((cos, sin) if cos is not None else ())
+    _check_device(tensors, q.device)
+    if qn is None and kn is None:
+        return torch.ops.kfmi.norm_rope(q, k, gq, gk, cos, sin, norm_style)
+    qn = torch.empty_like(q) if qn is None else qn
+    kn = torch.empty_like(k) if kn is None else kn
+    _norm_rope_into(q, k, gq, gk, cos, sin, qn, kn, norm_style)
+    return qn, kn
+
+
+def _norm_rope_into(q, k, gq, gk, cos, sin, qn, kn, norm_style):
+    b, h, s, d = q.shape
+    rope = cos is not None
+    _lib.call("kfmi_prepare_bf16", ptr(q), ptr(k), ptr(gq), ptr(gk), ptr(cos), ptr(sin), ptr(qn), ptr(kn),
+              b, h, k.shape[1], s, d, EPS, NORM_STYLES[norm_style], PREP_ROPE if rope else 0, stream_of(q))
+
+
+def factored_qk_attention(q, k, v, gq, gk, *, causal=False):
+    """Allocating form of ``launch_factored_attention``: returns ``(out, inv, kn)``."""
+    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
+        raise ValueError("Expected q [B,Hq,S,D] and k, v [B,Hkv,S,D]")
+    b, h, s, d = q.shape
+    if (d not in (128, 256) or k.shape[0] != b or tuple(k.shape[2:]) != (s, d) or h % k.shape[1]
+            or tuple(gq.shape) != (d,) or tuple(gk.shape) != (d,)):
+        raise ValueError("Expected D in (128, 256), matching shapes, gamma vectors [D] and valid GQA")
+    _check_device((q, k, v, gq, gk), q.device)
+    return torch.ops.kfmi.factored_attention(q, k, v, gq, gk, bool(causal))
+
+
+# ---------------------------------------------------------------------------
+# torch.library custom ops (graph-capturable: no host sync, launches on the
+# current stream; fake kernels give shapes to tracing)
+# ---------------------------------------------------------------------------
+
+@torch.library.custom_op("kfmi::optimized_attention", mutates_args=(), device_types="cuda")
+def _optimized_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor,
+                            gk: torch.Tensor, cos: Optional[torch.Tensor], sin: Optional[torch.Tensor],
+                            causal: bool, mode: str, bn: int, norm_style: str) -> torch.Tensor:
+    out = torch.empty_like(q)
+    kn = torch.empty_like(k)
+    qn = torch.empty_like(q) if mode == "unfused" else None
+    rotary = cos is not None
+    xs = (q, k, v, gq, gk, cos if rotary else q, sin if rotary else k)
+    with torch.cuda.device(q.device):
+        launch_attention(xs, out, causal=causal, mode=mode, bm=128, bn=bn, rope=rotary, qn=qn, kn=kn,
+                         norm_style=norm_style)
+    return out
+
+
+@_optimized_attention_op.register_fake
+def _(q, k, v, gq, gk, cos, sin, causal, mode, bn, norm_style):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("kfmi::norm_rope", mutates_args=(), device_types="cuda")
+def _norm_rope_op(q: torch.Tensor, k: torch.Tensor, gq: torch.Tensor, gk: torch.Tensor,
+                  cos: Optional[torch.Tensor], sin: Optional[torch.Tensor],
+                  norm_style: str) -> tuple[torch.Tensor, torch.Tensor]:
+    qn = torch.empty_like(q)
+    kn = torch.empty_like(k)
+    with torch.cuda.device(q.device):
+        _norm_rope_into(q, k, gq, gk, cos, sin, qn, kn, norm_style)
+    return qn, kn
+
+
+@_norm_rope_op.register_fake
+def _(q, k, gq, gk, cos, sin, norm_style):
+    return torch.empty_like(q), torch.empty_like(k)
+
+
+@torch.library.custom_op("kfmi::factored_attention", mutates_args=(), device_types="cuda")
+def _factored_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, gq: torch.Tensor, gk: torch.Tensor,
+                 causal: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    out = torch.empty_like(q)
+    kn = torch.empty_like(k)
+    inv = torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32)
+    with torch.cuda.device(q.device):
+        launch_factored_attention((q, k, v, gq, gk), out, inv, kn, causal=causal, bm=128, bn=64)
+    return out, inv, kn
+
+
+@_factored_op.register_fake
+def _(q, k, v, gq, gk, causal):
+    return (torch.empty_like(q), torch.empty(q.shape[:-1], device=q.device, dtype=torch.float32),
+            torch.empty_like(k))
+
+
+def attention_flops(b: int, hq: int, s: int, d: int, causal: bool) -> int:
+    """Algorithmic FLOPs of QK^T and PV: 4*B*Hq*D*pairs, pairs = S(S+1)/2 causal, S^2 otherwise."""
+    pairs = s * (s + 1) // 2 if causal else s * s
+    return 4 * b * hq * d * pairs
+
+
+def norm_rope_bytes(b: int, hq: int, hkv: int, s: int, d: int, rope: bool = True) -> int:
+    """Algorithmic HBM bytes of one Q+K norm+RoPE pass: BF16 read+write of every
+    row, the cos/sin half-tables and both gamma vectors."""
+    return 4 * b * s * (hq + hkv) * d + (2 * s * d if rope else 0) + 4 * d
+
+
+def k_prep_bytes(b: int, hkv: int, s: int, d: int, rope: bool = True) -> int:
+    return 4 * b * s * hkv * d + (2 * s * d if rope else 0) + 2 * d
+

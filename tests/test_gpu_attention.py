@@ -1,0 +1,134 @@
+"""GPU parity of the fused-prologue GQA flash-attention prefill against the CPU
+FP32 oracle (src/e1_rope_publication_v1.py:295-302) on the same seeded inputs.
+
+Gates: attention max-abs <= 2e-2 plus the reference metric (finite,
+allclose atol=rtol=.025, relative-L2 <= .025) for the FP32 prologue; the
+reference metric alone for the HF prologue (the reference's own API checks,
+src/e4_model_shapes_publication_v2.py:263-283, use the HF style).  Full-length
+sequences (S=4096, 8192) are checked on a sample of query rows that always
+includes the first and last rows.
+"""
+import pytest
+import torch
+
+import oracle
+from helpers import announce
+from kernelfuser_amd import QWEN3_8B, launch_attention, make_inputs, optimized_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(xs_gpu, causal, mode="query", bn=128, norm_style="fp32", rope=True):
+    args = (xs_gpu.q, xs_gpu.k, xs_gpu.v, xs_gpu.gq, xs_gpu.gk) + ((xs_gpu.cos, xs_gpu.sin) if rope else ())
+    out = optimized_attention(*args, causal=causal, mode=mode, bn=bn, norm_style=norm_style)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def test_config3_s2048_causal_fp32(gpu):
+    """Config 3: B=1, S=2048, Qwen3-8B, causal, theta=1e6."""
+    xs = make_inputs(1, 2048, QWEN3_8B, 1909)
+    announce("attention query fp32 B=1 S=2048 causal")
+    out = _run(xs.to(gpu), True)
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.attention_gate(out, ref)
+    assert m["pass"], m
+
+
+@pytest.mark.parametrize("s", [33, 129])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("mode", ["query", "unfused"])
+@pytest.mark.parametrize("bn", [64, 128])
+def test_api_tails_hf(gpu, s, causal, mode, bn):
+    """Public-API checks of the reference (e4:263-283): S in {33,129} x causal x
+    {query, unfused} x BN {64,128}, Qwen3-8B RoPE with the HF style."""
+    xs = make_inputs(1, s, QWEN3_8B, 9909)
+    announce(f"attention {mode} hf S={s} causal={causal} bn={bn}")
+    out = _run(xs.to(gpu), causal, mode=mode, bn=bn, norm_style="hf")
+    ref = oracle.oracle_fp32(*xs.astuple(), causal)
+    m = oracle.metric(out, ref)
+    assert m["pass"], m
+
+
+@pytest.mark.parametrize("s", [33, 129])
+@pytest.mark.parametrize("causal", [False, True])
+def test_api_tails_norope_legacy(gpu, s, causal):
+    """The reference's no-RoPE API rows use Gemma-3-4B (8,4,256) with 'legacy'."""
+    xs = make_inputs(1, s, (8, 4, 256), 9909, rope=False)
+    announce(f"attention query legacy no-rope D=256 S={s} causal={causal}")
+    out = _run(xs.to(gpu), causal, norm_style="legacy", rope=False)
+    ref = oracle.refinement_oracle_norope(xs.q, xs.k, xs.v, xs.gq, xs.gk, causal)
+    m = oracle.metric(out, ref)
+    assert m["pass"], m
+
+
+def test_ragged_b4_s1000(gpu):
+    """Config 4 ragged case: B=4, S=1000 (non-multiple-of-64 tail), causal."""
+    xs = make_inputs(4, 1000, QWEN3_8B, 2909)
+    announce("attention query fp32 B=4 S=1000 causal")
+    out = _run(xs.to(gpu), True)
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.attention_gate(out, ref)
+    assert m["pass"], m
+
+
+@pytest.mark.parametrize("s", [4096, 8192])
+def test_long_causal_row_sample(gpu, s):
+    """Config 4 long shapes: rows sampled across the sequence, incl. first/last."""
+    xs = make_inputs(1, s, QWEN3_8B, 3909)
+    announce(f"attention query fp32 B=1 S={s} causal")
+    out = _run(xs.to(gpu), True)
+    gen = torch.Generator().manual_seed(s)
+    rows = torch.unique(torch.cat([torch.arange(0, 4), torch.randint(0, s, (40,), generator=gen),
+                                   torch.arange(s - 4, s)]))
+    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
+    m = oracle.attention_gate(out[:, :, rows], ref)
+    assert m["pass"], m
+
+
+def test_noncausal_unfused_fp32(gpu):
+    xs = make_inputs(2, 300, QWEN3_8B, 1701)
+    announce("attention unfused fp32 B=2 S=300 non-causal")
+    out = _run(xs.to(gpu), False, mode="unfused")
+    ref = oracle.oracle_fp32(*xs.astuple(), False)
+    m = oracle.attention_gate(out, ref)
+    assert m["pass"], m
+
+
+def test_gqa_head_mapping(gpu):
+    """Each KV head's V is a distinct constant; Q head h must return the constant
+    of KV head h // (Hq/Hkv) (rope:616)."""
+    xs = make_inputs(1, 160, QWEN3_8B, 77)
+    consts = torch.arange(1, 9, dtype=torch.float32) / 8.0
+    xs.v = consts.view(1, 8, 1, 1).expand(1, 8, 160, 128).to(torch.bfloat16).contiguous()
+    announce("attention GQA mapping")
+    out = _run(xs.to(gpu), True)
+    want = consts.repeat_interleave(4).view(1, 32, 1, 1).expand_as(out)
+    assert float((out.float() - want).abs().max()) < 1e-2
+
+
+def test_causal_row0_is_v0(gpu):
+    xs = make_inputs(1, 70, QWEN3_8B, 78)
+    announce("attention causal row 0")
+    out = _run(xs.to(gpu), True)
+    want = oracle.expand(xs.v.float(), 32)[:, :, 0]
+    assert float((out[:, :, 0].float() - want).abs().max()) < 1e-2
+
+
+def test_launch_attention_buffers(gpu):
+    """launch_attention writes out and the K scratch; 'full' is refused, missing
+    scratch raises ValueError (rope:668-672)."""
+    xs = make_inputs(1, 96, QWEN3_8B, 5).to(gpu)
+    out = torch.empty_like(xs.q)
+    kn = torch.empty_like(xs.k)
+    announce("launch_attention query")
+    launch_attention(xs.reference7, out, causal=True, mode="query", kn=kn, norm_style="fp32")
+    torch.cuda.synchronize()
+    kref = oracle.norm_rope_fp32(xs.k.cpu(), xs.gk.cpu(), xs.cos.cpu(), xs.sin.cpu())
+    assert oracle.norm_rope_gate(kn.cpu(), kref)["pass"]
+    ref = oracle.oracle_fp32(*[t.cpu() for t in xs.astuple()], True)
+    assert oracle.attention_gate(out.cpu(), ref)["pass"]
+    with pytest.raises(ValueError):
+        launch_attention(xs.reference7, out, mode="unfused", kn=kn)
+    with pytest.raises(ValueError):
+        launch_attention(xs.reference7, out, mode="bad", kn=kn)

@@ -1,0 +1,122 @@
+"""GPU parity of the row-preparation kernel (per-head Q/K RMSNorm + RoPE) against
+the CPU FP32 oracle, on the same seeded BF16 inputs.
+
+Gates: FP32 style within max-abs 1.6e-2 and mean-abs 2e-3 of the FP32 oracle
+(north-star gate) and the reference metric; the HF and legacy styles match the
+oracle's BF16-boundary restatement to within one BF16 ulp on a vanishing
+fraction of elements (only an FP32 last-bit difference of the inverse RMS can
+move a rounding).
+"""
+import pytest
+import torch
+
+import oracle
+from helpers import announce, bf16_ulp
+from kernelfuser_amd import QWEN3_8B, GEMMA3_12B, make_inputs, norm_rope, prepare_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_fp32(xs):
+    return (oracle.norm_rope_fp32(xs.q, xs.gq, xs.cos, xs.sin), oracle.norm_rope_fp32(xs.k, xs.gk, xs.cos, xs.sin))
+
+
+def _oracle_chain(xs, style):
+    """Oracle chain outputs and, per element, the magnitude max(|n_d|, |n_partner|)
+    of the two normalised values the rotation combines."""
+    norm = oracle.norm_hf_bf16 if style == "hf" else oracle.norm_legacy_bf16
+    out = []
+    for x, g in ((xs.q, xs.gq), (xs.k, xs.gk)):
+        y = norm(x, g)
+        half = y.shape[-1] // 2
+        scale = torch.maximum(y.float().abs(), torch.cat([y[..., half:], y[..., :half]], -1).float().abs())
+        out.append((oracle.rope_hf_bf16(y, xs.cos, xs.sin) if xs.cos is not None else y, scale))
+    return out
+
+
+@pytest.mark.parametrize("seed", [1701, 2803, 3907])
+def test_config1_fp32_gate(gpu, seed):
+    """Config 1: B=1, S=128, Qwen3-8B heads, theta=1e6; FP32 style passes the gate."""
+    xs = make_inputs(1, 128, QWEN3_8B, seed)
+    announce(f"norm_rope fp32 B=1 S=128 seed={seed}")
+    qn, kn = norm_rope(*[t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)], norm_style="fp32")
+    torch.cuda.synchronize()
+    rq, rk = _oracle_fp32(xs)
+    for got, ref in ((qn, rq), (kn, rk)):
+        m = oracle.norm_rope_gate(got.cpu(), ref)
+        assert m["pass"], m
+
+
+@pytest.mark.parametrize("style", ["hf", "legacy"])
+@pytest.mark.parametrize("b,s,geom", [(1, 128, QWEN3_8B), (2, 33, QWEN3_8B), (1, 129, GEMMA3_12B)])
+def test_bf16_chain_styles(gpu, style, b, s, geom):
+    """HF / legacy rounding chains equal the oracle's restated chain (<= 1 ulp, rare)."""
+    xs = make_inputs(b, s, geom, 4909)
+    announce(f"norm_rope {style} B={b} S={s} geom={geom}")
+    qn, kn = norm_rope(*[t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)], norm_style=style)
+    torch.cuda.synchronize()
+    for got, (ref, scale) in zip((qn.cpu(), kn.cpu()), _oracle_chain(xs, style)):
+        # A last-bit difference of the FP32 inverse RMS can flip one rounding of a
+        # normalised value or RoPE product (one ulp of |n|), plus the final rounding.
+        diff = (got.float() - ref.float()).abs()
+        tol = bf16_ulp(scale) + bf16_ulp(ref)
+        assert bool((diff <= tol).all()), float((diff / tol).max())
+        assert float((diff > 0).float().mean()) < 2e-3
+
+
+@pytest.mark.parametrize("b,s,geom", [(1, 33, QWEN3_8B), (1, 129, QWEN3_8B), (2, 64, GEMMA3_12B)])
+def test_tails_and_d256_fp32(gpu, b, s, geom):
+    xs = make_inputs(b, s, geom, 13109)
+    announce(f"norm_rope fp32 tails B={b} S={s} geom={geom}")
+    qn, kn = norm_rope(*[t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)], norm_style="fp32")
+    torch.cuda.synchronize()
+    rq, rk = _oracle_fp32(xs)
+    for got, ref in ((qn, rq), (kn, rk)):
+        m = oracle.norm_rope_gate(got.cpu(), ref)
+        assert m["pass"], m
+
+
+def test_no_rope_norm_only(gpu):
+    xs = make_inputs(1, 96, QWEN3_8B, 2909, rope=False)
+    announce("norm_rope fp32 no-rope")
+    qn, kn = norm_rope(*[t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk)], norm_style="fp32")
+    torch.cuda.synchronize()
+    for got, x, g in ((qn, xs.q, xs.gq), (kn, xs.k, xs.gk)):
+        m = oracle.norm_rope_gate(got.cpu(), oracle.norm_fp32(x, g))
+        assert m["pass"], m
+
+
+def test_prepare_only_k_leaves_q(gpu):
+    """prepare_attention(only_k=True) writes K rows only (rope:591-595)."""
+    xs = make_inputs(1, 200, QWEN3_8B, 3907).to(gpu)
+    qn = torch.full_like(xs.q, 7.0)
+    kn = torch.empty_like(xs.k)
+    announce("prepare only_k")
+    prepare_attention(xs.reference7, qn, kn, only_k=True, rope=True, norm_style="fp32")
+    torch.cuda.synchronize()
+    assert bool((qn == 7.0).all())
+    ref = oracle.norm_rope_fp32(xs.k.cpu(), xs.gk.cpu(), xs.cos.cpu(), xs.sin.cpu())
+    assert oracle.norm_rope_gate(kn.cpu(), ref)["pass"]
+
+
+@pytest.mark.parametrize("b,s", [(1, 8192), (16, 512)])
+def test_full_size_row_sample(gpu, b, s):
+    """Bandwidth-sweep shapes: every launch covers all rows; a row sample is
+    checked against the oracle and the RoPE pair-norm invariant holds everywhere."""
+    xs = make_inputs(b, s, QWEN3_8B, 1909)
+    g = [t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)]
+    announce(f"norm_rope fp32 full size B={b} S={s}")
+    qn, kn = norm_rope(*g, norm_style="fp32")
+    torch.cuda.synchronize()
+    rows = torch.unique(torch.cat([torch.arange(0, 8), torch.randint(0, s, (120,), generator=torch.Generator().manual_seed(5)),
+                                   torch.arange(s - 8, s)]))
+    for got, x, gam in ((qn, xs.q, xs.gq), (kn, xs.k, xs.gk)):
+        ref = oracle.rope_fp32(oracle.norm_fp32(x[:, :, rows], gam), xs.cos[rows], xs.sin[rows])
+        m = oracle.norm_rope_gate(got[:, :, rows.to(gpu)].cpu(), ref)
+        assert m["pass"], m
+    # pair-norm invariant on the whole tensor (rotation preserves |(y_i, y_i+64)|)
+    d = 128
+    nq = (g[0].float() * torch.rsqrt(g[0].float().square().mean(-1, keepdim=True) + 1e-6) * g[2].float())
+    pre = nq[..., : d // 2].square() + nq[..., d // 2:].square()
+    post = qn.float()[..., : d // 2].square() + qn.float()[..., d // 2:].square()
+    assert bool(((post - pre).abs() <= pre * 2.0 ** -6 + 1e-3).all())
