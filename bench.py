@@ -1,0 +1,323 @@
+#!/usr/bin/env python3
+"""Benchmark of the RoPE-aware attention prologue on one MI355X (gfx950).
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+Headline workload (``value``): the ``optimized_attention`` query path of the
+reference (src/e1_rope_publication_v1.py:661-726) at Qwen3-8B per-layer shape,
+B=1, S=4096, causal, theta=1e6 -- one step = both launches of
+``launch_attention(mode='query')`` (K RMSNorm+RoPE once, then causal GQA flash
+attention with Q's RMSNorm+RoPE in the prologue), the reference's timing unit
+(rope:665-666).  ``value`` is causal TFLOP/s (4*B*Hq*D*S(S+1)/2 per step) over
+the K timed steps, inputs resident in HBM.
+
+The same line carries, as nested objects:
+  * ``roofline``      -- the attention kernel alone, timed with HIP events on the
+                         stream it is launched on, against dense-BF16 MFMA peak;
+  * ``norm_rope``     -- the isolated Q/K RMSNorm+RoPE bandwidth sweep (six
+                         shapes), rotating buffer sets so the 256 MB Infinity
+                         Cache cannot serve replays, against HBM peak;
+  * ``prefill_shapes``-- S=2048, S=8192 and the ragged B=4,S=1000 prefill;
+  * ``factored``      -- the no-RoPE factored launch (Hq16/Hkv8/D256, B=2, S=2048);
+  * ``cpu_baseline``  -- the eager FP32 CPU path (the oracle), timed on the host
+                         cores on a bounded sample of the headline workload, and
+                         the parity of the GPU output on that sample.
+
+Inputs are synthetic (seeded CPU generator, BF16, copied to the GPU).  Only
+one GPU is supported.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "µs + HBM GB/s fused QK-norm+RoPE; TFLOP/s fused-prologue GQA prefill"
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense BF16 MFMA, published
+SWEEP = [(1, 512), (1, 2048), (1, 8192), (4, 2048), (8, 1024), (16, 512)]
+QWEN3_8B = (32, 8, 128)
+GEMMA3_12B = (16, 8, 256)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100, help="timed steps of the headline workload")
+    ap.add_argument("--warmup", type=int, default=300,
+                    help="untimed steps first; the GPU clock needs tens of ms of load to settle")
+    ap.add_argument("--seq", type=int, default=4096, help="headline sequence length")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--norm-style", default="fp32", choices=["fp32", "hf", "legacy"])
+    ap.add_argument("--quick", action="store_true", help="headline workload only (no sweep, extra shapes, CPU)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget per workload")
+    ap.add_argument("--pmc", action="store_true",
+                    help="short run for rocprofv3 counter passes: a few launches of each kernel plus a "
+                         "copy of known size for calibration; prints a JSON line of what ran")
+    return ap.parse_args()
+
+
+def _events():
+    import torch
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_launches(fn, n, warmup=3):
+    """Average device time (ms) of ``fn`` over ``n`` back-to-back calls, measured
+    with HIP events on torch's current stream (the stream the kernels use)."""
+    import torch
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    a, b = _events()
+    a.record()
+    for i in range(n):
+        fn(i)
+    b.record()
+    b.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def load_traffic():
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return {}
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return {}
+
+
+def headline(args, torch, kf):
+    """Timed steps of launch_attention(mode='query') plus the attention kernel alone."""
+    b, s = args.batch, args.seq
+    hq, hkv, d = QWEN3_8B
+    xs_cpu = kf.make_inputs(b, s, QWEN3_8B, 1909)
+    xs = xs_cpu.to("cuda:0")
+    out = torch.empty_like(xs.q)
+    kn = torch.empty_like(xs.k)
+    step = lambda: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn,
+                                       norm_style=args.norm_style)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = _events()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    dev_ms = ev0.elapsed_time(ev1)
+    flops = kf.attention_flops(b, hq, s, d, True)
+    ms_step = wall_ms / args.steps
+    res = {"flops_per_step": flops, "ms_per_step": ms_step, "device_ms_per_step": dev_ms / args.steps,
+           "tflops": flops / (ms_step * 1e-3) / 1e12}
+    # The two kernels separately (events on the launch stream).
+    attn_ms = time_launches(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
+                                                           causal=True, fuse_q=True, norm_style=args.norm_style),
+                            max(args.steps, 20))
+    prep_ms = time_launches(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
+                                                           norm_style=args.norm_style), max(args.steps, 20))
+    res["attention_kernel_us"] = attn_ms * 1e3
+    res["k_prep_kernel_us"] = prep_ms * 1e3
+    res["attention_kernel_tflops"] = flops / (attn_ms * 1e-3) / 1e12
+    res["k_prep_gbs"] = kf.k_prep_bytes(b, hkv, s, d) / (prep_ms * 1e-3) / 1e9
+    return res, xs_cpu, out
+
+
+def norm_rope_sweep(args, torch, kf):
+    """Isolated Q+K norm+RoPE, one launch per call, buffer sets rotated (> 512 MB total)."""
+    hq, hkv, d = QWEN3_8B
+    rows = []
+    for b, s in SWEEP:
+        nbytes = kf.norm_rope_bytes(b, hq, hkv, s, d)
+        nsets = max(2, min(64, -(-768 * 2 ** 20 // nbytes)))
+        base = kf.make_inputs(b, s, QWEN3_8B, 1909, with_v=False).to("cuda:0")
+        sets = []
+        for i in range(nsets):
+            q = base.q if i == 0 else base.q.roll(i, dims=2).contiguous()
+            k = base.k if i == 0 else base.k.roll(i, dims=2).contiguous()
+            sets.append((q, k, torch.empty_like(q), torch.empty_like(k)))
+        fn = lambda i: kf.norm_rope(sets[i % nsets][0], sets[i % nsets][1], base.gq, base.gk, base.cos, base.sin,
+                                    norm_style=args.norm_style, qn=sets[i % nsets][2], kn=sets[i % nsets][3])
+        n = max(4 * nsets, 40)
+        ms = time_launches(fn, n, warmup=nsets)
+        rows.append({"B": b, "S": s, "bytes": nbytes, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+                     "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "buffer_sets": nsets})
+        del sets, base
+        torch.cuda.empty_cache()
+    big = [r for r in rows if r["bytes"] > 100e6]
+    best = max(big, key=lambda r: r["gbs"])
+    return {"kernel": "rows_kernel (Q+K rows, one launch)", "norm_style": args.norm_style, "shapes": rows,
+            "roofline": {"bound": "hbm", "achieved": best["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": best["gbs"] / HBM_PEAK_GBS, "shape": [best["B"], best["S"]],
+                         "traffic": load_traffic().get("norm_rope_b%d_s%d" % (best["B"], best["S"]))},
+            "min_frac_large_shapes": min(r["frac_hbm"] for r in big)}
+
+
+def prefill_shapes(args, torch, kf):
+    hq, hkv, d = QWEN3_8B
+    rows = []
+    for b, s in [(1, 2048), (1, 8192), (4, 1000)]:
+        xs = kf.make_inputs(b, s, QWEN3_8B, 2909).to("cuda:0")
+        out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+        ms = time_launches(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
+                                                          bn=64, kn=kn, norm_style=args.norm_style), 20)
+        f = kf.attention_flops(b, hq, s, d, True)
+        rows.append({"B": b, "S": s, "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
+                     "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS})
+        del xs, out, kn
+    return rows
+
+
+def factored(args, torch, kf):
+    b, s = 2, 2048
+    hq, hkv, d = GEMMA3_12B
+    xs = kf.make_inputs(b, s, GEMMA3_12B, 1909, rope=False).to("cuda:0")
+    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    inv = torch.empty(xs.q.shape[:-1], device="cuda:0", dtype=torch.float32)
+    ms = time_launches(lambda i: kf.launch_factored_attention((xs.q, xs.k, xs.v, xs.gq, xs.gk), out, inv, kn,
+                                                              causal=True, bm=128, bn=64), 20)
+    f = kf.attention_flops(b, hq, s, d, True)
+    return {"B": b, "S": s, "Hq": hq, "Hkv": hkv, "D": d, "causal": True, "us": ms * 1e3,
+            "tflops": f / (ms * 1e-3) / 1e12, "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS}
+
+
+def cpu_baseline(args, torch, xs_cpu, out_gpu):
+    """The eager FP32 CPU path (oracle restatement of rope:295-302) on a bounded
+    sample of the headline workload: KV group 0 (Q heads 0-3, KV head 0) of
+    B=1, S=seq.  Also checks the GPU output on that sample (attention gate)."""
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    hq, hkv, d = QWEN3_8B
+    g = hq // hkv
+    q, k, v = xs_cpu.q[:, :g].contiguous(), xs_cpu.k[:, :1].contiguous(), xs_cpu.v[:, :1].contiguous()
+    times, ref = [], None
+    t_end = time.perf_counter() + args.cpu_seconds
+    while time.perf_counter() < t_end or len(times) < 2:
+        t0 = time.perf_counter()
+        ref = oracle.oracle_fp32(q, k, v, xs_cpu.gq, xs_cpu.gk, xs_cpu.cos, xs_cpu.sin, True)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    f = 4 * q.shape[0] * g * d * (q.shape[2] * (q.shape[2] + 1) // 2)
+    med = statistics.median(times[1:] if len(times) > 2 else times)
+    gate = oracle.attention_gate(out_gpu[:, :g].float().cpu(), ref)
+    res = {"value": f / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": (f"oracle_fp32 (eager FP32 torch: RMSNorm, RoPE, SDPA) on KV group 0 of the headline "
+                      f"workload: B=1, Hq=4, Hkv=1, S={q.shape[2]}, D=128, causal; {len(times)} calls in "
+                      f"{sum(times):.1f} s, median {med * 1e3:.1f} ms"),
+           "parity": {k2: gate[k2] for k2 in ("max_abs", "mean_abs", "relative_l2", "pass")}}
+    # norm+RoPE CPU leg on the largest sweep shape, in GB/s.
+    nr = None
+    xs = None
+    try:
+        from kernelfuser_amd.inputs import make_inputs
+        xs = make_inputs(1, 8192, QWEN3_8B, 1909, with_v=False)
+        nt = []
+        t_end = time.perf_counter() + args.cpu_seconds / 2
+        while time.perf_counter() < t_end or len(nt) < 2:
+            t0 = time.perf_counter()
+            oracle.norm_rope_fp32(xs.q, xs.gq, xs.cos, xs.sin).to(torch.bfloat16)
+            oracle.norm_rope_fp32(xs.k, xs.gk, xs.cos, xs.sin).to(torch.bfloat16)
+            nt.append(time.perf_counter() - t0)
+            if len(nt) >= 50:
+                break
+        m = statistics.median(nt[1:] if len(nt) > 2 else nt)
+        by = 4 * 8192 * 40 * 128 + 2 * 8192 * 128 + 4 * 128
+        nr = {"value": by / m / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+              "sample": f"norm_rope_fp32 of Q and K at B=1, S=8192 (Qwen3-8B heads), {len(nt)} calls, "
+                        f"median {m * 1e3:.1f} ms"}
+    finally:
+        del xs
+    res["norm_rope"] = nr
+    return res
+
+
+def pmc_run(torch, kf):
+    """A few launches of each kernel at the headline shapes plus one copy of
+    known size, for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE)."""
+    xs = kf.make_inputs(1, 4096, QWEN3_8B, 1909).to("cuda:0")
+    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    for _ in range(3):
+        kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn, norm_style="fp32")
+    nr = kf.make_inputs(1, 8192, QWEN3_8B, 1909, with_v=False).to("cuda:0")
+    qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
+    for _ in range(3):
+        kf.norm_rope(nr.q, nr.k, nr.gq, nr.gk, nr.cos, nr.sin, norm_style="fp32", qn=qn, kn=kn2)
+    src = torch.ones(256 * 2 ** 20 // 4, device="cuda:0", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_run": True, "copy_bytes_each_way": src.numel() * 4,
+                      "attention": "B=1 S=4096 causal", "norm_rope": "B=1 S=8192"}), flush=True)
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (multi-GPU sharding is "
+                                   "a design note, not built)", "n_gpus": args.gpus}), flush=True)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible; bench.py needs an MI355X"}), flush=True)
+        sys.exit(1)
+    sys.path.insert(0, str(ROOT))
+    import kernelfuser_amd as kf
+    from kernelfuser_amd import _lib
+    _lib.load()
+    if args.pmc:
+        pmc_run(torch, kf)
+        return
+    head, xs_cpu, out = headline(args, torch, kf)
+    traffic = load_traffic().get("attention_b%d_s%d" % (args.batch, args.seq))
+    line = {
+        "metric": METRIC,
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded CPU torch.Generator, N(0,1) Q/K/V, gamma=1+0.1N, theta=1e6)",
+        "config": {"workload": "optimized_attention mode=query (K norm+RoPE launch + fused-prologue causal "
+                               "GQA prefill), Qwen3-8B per-layer heads",
+                   "B": args.batch, "S": args.seq, "Hq": 32, "Hkv": 8, "D": 128, "causal": True,
+                   "norm_style": args.norm_style, "flops_per_step": head["flops_per_step"],
+                   "flops_convention": "4*B*Hq*D*S(S+1)/2"},
+        "roofline": {"bound": "mfma", "kernel": "attn_fwd_kernel (fused Q norm+RoPE prologue)",
+                     "achieved": head["attention_kernel_tflops"], "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
+                     "frac": head["attention_kernel_tflops"] / MFMA_BF16_PEAK_TFS,
+                     "kernel_us": head["attention_kernel_us"], "traffic": traffic},
+        "kernels": {"attention_us": head["attention_kernel_us"], "k_prep_us": head["k_prep_kernel_us"],
+                    "k_prep_gbs": head["k_prep_gbs"], "device_ms_per_step": head["device_ms_per_step"]},
+    }
+    if not args.quick:
+        line["norm_rope"] = norm_rope_sweep(args, torch, kf)
+        line["prefill_shapes"] = prefill_shapes(args, torch, kf)
+        line["factored"] = factored(args, torch, kf)
+    if not args.quick and not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args, torch, xs_cpu, out)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -102,6 +102,18 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
               _bm(bm), _bn(bn), stream_of(q))
 
 
+def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=False, fuse_q=True,
+                      norm_style="fp32", bm=128, bn=64, scale=None):
+    """The attention launch alone (attention_v2_kernel, rope:608-649) on a prepared
+    ``kn``.  ``fuse_q=True``: raw ``q`` with its RMSNorm (``gq``) and, when both
+    tables are given, RoPE in the prologue (FUSE_Q); ``fuse_q=False``: ``q`` is
+    already prepared.  ``scale`` defaults to D^-1/2 (rope:676)."""
+    b, h, s, d = q.shape
+    _lib.call("kfmi_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(gq), ptr(cos), ptr(sin), ptr(out),
+              b, h, kn.shape[1], s, d, float(d) ** -0.5 if scale is None else float(scale), EPS,
+              int(bool(causal)), int(bool(fuse_q)), NORM_STYLES[norm_style], _bm(bm), _bn(bn), stream_of(q))
+
+
 def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=64):
     """No-RoPE factored launch (qk:641-652): ``kn = bf16(k*inv_k*gk*gq)`` and FP32
     ``inv`` ``[B,Hq,S]`` (Q's inverse RMS, applied to the scores) are written to the
