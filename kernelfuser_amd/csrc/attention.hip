@@ -18,10 +18,22 @@
 //                               ds_read_b64_tr_b16 (transpose on read),
 //                           B = P^T straight from the GEMM1 accumulator
 //                               (exp2, cvt to bf16, no data movement).
-// MFMA: v_mfma_f32_32x32x16_bf16.  Operand layouts (verified on the device):
-//   A[m][k] -> lane m + 32*(k/8), element k%8; B[k][n] -> lane n + 32*(k/8),
-//   element k%8; C[m][n] -> lane n + 32*((m/4)%2), register 8*(m/8)... i.e.
-//   register (m/8)*4 + m%4.
+// MFMA: v_mfma_f32_32x32x16_bf16.  Operand layouts: A[m][k] -> lane
+// m + 32*(k/8), element k%8; B[k][n] -> lane n + 32*(k/8), element k%8;
+// C[m][n] -> lane n + 32*((m/4)%2), register (m/8)*4 + m%4.
+//
+// K/V staging: tiles of BN rows (16 KiB each) are copied HBM -> LDS by the
+// buffer unit (buffer_load_dwordx4 ... lds: lane L of a load writes LDS bytes
+// base + 16*L), so no VGPRs, no ds_write and no bounds branches are spent on
+// staging: rows past S lie outside the buffer descriptor's range and arrive as
+// zeros.  Both K and V are double-buffered; the 16-byte chunks of each row are
+// XOR-swizzled (K: chunk ^ (row & 7); V: chunk ^ 2*(row & 3)) so the GEMM1
+// row reads and the GEMM2 transpose reads are bank-conflict free.
+//
+// Pipeline (one barrier per KV tile): iteration t issues the copies of K(t+2)
+// and V(t+1), then GEMM1 of tile t+1 and the softmax + GEMM2 of tile t, so the
+// exp2/max/sum VALU work of tile t overlaps the MFMAs of tile t+1 and each
+// copy has a full iteration to land.
 //
 // Q prologue (query fusion): the wave's raw Q rows are loaded straight into
 // the B-operand layout (lane: row lane%32, columns 16c + 8*(lane/32) + 0..7),
@@ -30,10 +42,14 @@
 // the rounding points of the selected style, then round once to BF16.
 //
 // Softmax: exp2 online softmax with scale*log2(e) folded into one FMA per
-// score (rope:636-643); the O rescale is skipped when no row max of the wave
-// grew.  Causal: the KV loop stops at the diagonal, masks are applied only on
-// diagonal/tail tiles, waves skip tiles that are fully masked for their rows,
-// and the grid issues the longest query blocks first.
+// score (rope:636-643).  The running max is raised only when a row's tile max
+// exceeds it by more than 2^8 (log2 domain) -- probabilities then stay below
+// 256, far inside FP32/BF16 range, and O is rescaled a handful of times per
+// row instead of on every tile; after the final division by the row sum the
+// result is the same softmax.  Causal: the KV loop stops at the diagonal,
+// masks are applied only on diagonal/tail tiles, waves skip tiles that are
+// fully masked for their rows, and the grid issues the longest query blocks
+// first.
 #include <math.h>
 
 #include "kfmi_device.h"
@@ -70,26 +86,60 @@ __device__ __forceinline__ float rope_elem(float n, float np, float c, float s, 
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const u32x4_t &w) { return __builtin_bit_cast(bf16x8_t, w); }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor of a byte range: raw addressing, reads at or past `bytes`
+// return zeros.
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)(uint32_t)(a >> 32);  // stride 0
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from buffer offset voff + soff into LDS at lds + 16*lane.
+// Issued as inline assembly so the compiler does not guard every later LDS
+// read with a wait for it; the kernel orders copies and reads itself
+// (wait_copies + barrier).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; it is set right here
+__device__ __forceinline__ void copy16_to_lds(const i32x4_t &rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until every copy this wave issued has landed in LDS.
+__device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+constexpr float RESCALE_SLACK = 8.0f;  // log2 units: probabilities stay <= 2^8
+
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
 __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnParams p) {
-  constexpr int BM = 128;          // query rows per workgroup (4 waves x 32)
-  constexpr int NT = 256;          // threads
-  constexpr int KST = D + 8;       // K tile row stride (elements): +16 B -> conflict-free b128 reads
-  constexpr int VST = D + 16;      // V tile row stride: +32 B -> conflict-free transpose reads
-  constexpr int NC = D / 16;       // GEMM1 k-steps (16 columns of d)
-  constexpr int NDB = D / 32;      // GEMM2 output blocks (32 columns of d)
-  constexpr int NKB = BN / 32;     // GEMM1 output blocks (32 keys)
-  constexpr int NK16 = BN / 16;    // GEMM2 k-steps (16 keys)
-  constexpr int CPR = D / 8;       // 16-byte chunks per row
-  constexpr int LDC = BN * CPR / NT;  // 16-byte chunks per thread per tile (K and V each)
-  static_assert(LDC * NT == BN * CPR, "tile must split evenly over the workgroup");
+  constexpr int BM = 128;            // query rows per workgroup (4 waves x 32)
+  constexpr int RB = 2 * D;          // bytes per K/V row
+  constexpr int TILE = BN * RB;      // bytes per K or V tile
+  constexpr int NINST = TILE / 1024; // 1 KiB copies per tile
+  constexpr int LPW = NINST / 4;     // copies per wave per tile
+  constexpr int RPI = 1024 / RB;     // rows per copy
+  constexpr int CPR = D / 8;         // 16-byte chunks per row
+  constexpr int NC = D / 16;         // GEMM1 k-steps (16 columns of d)
+  constexpr int NDB = D / 32;        // GEMM2 output blocks (32 columns of d)
+  constexpr int NKB = BN / 32;       // GEMM1 output blocks (32 keys)
+  constexpr int NK16 = BN / 16;      // GEMM2 k-steps (16 keys)
+  constexpr int K0 = 0, K1 = TILE, V0 = 2 * TILE, V1 = 3 * TILE;
+  static_assert(TILE == 16384 && LPW * 4 == NINST, "tiles are 16 KiB, 4 copies per wave");
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[BN * KST];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[BN * VST];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5;   // half-wave: selects k-group of the MFMA operands
   const int lr = lane & 31;  // query row of this lane within the wave
   const int64_t S = p.S;
@@ -118,14 +168,49 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   const int64_t qoff = ((int64_t)b * p.Hq + h) * S;
   const int64_t kvoff = ((int64_t)b * p.Hkv + kvh) * S;
   const uint16_t *qbase = p.q + qoff * D;
-  const uint16_t *kbase = p.k + kvoff * D;
-  const uint16_t *vbase = p.v + kvoff * D;
   uint16_t *obase = p.out + qoff * D;
+
+  // Buffer descriptors of this head's K and V rows: reads at or past row S
+  // return zeros.
+  const uint32_t head_bytes = (uint32_t)(S * RB);
+  const i32x4_t krs = buffer_rsrc(p.k + kvoff * D, head_bytes);
+  const i32x4_t vrs = buffer_rsrc(p.v + kvoff * D, head_bytes);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
+
+  // Copy addressing: copy i of this wave fills LDS rows (w*LPW+i)*RPI + lane/CPR,
+  // slot lane%CPR, with the source chunk that the swizzle places there.
+  uint32_t kvo[LPW], vvo[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int row = (w * LPW + i) * RPI + lane / CPR;
+    const int slot = lane % CPR;
+    kvo[i] = (uint32_t)(row * RB + ((slot ^ (row & 7)) << 4));
+    vvo[i] = (uint32_t)(row * RB + ((slot ^ ((row & 3) << 1)) << 4));
+  }
+  auto copy_k = [&](int t, int buf) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) copy16_to_lds(krs, lds0 + buf + (w * LPW + i) * 1024, kvo[i], (uint32_t)(t * TILE));
+  };
+  auto copy_v = [&](int t, int buf) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) copy16_to_lds(vrs, lds0 + buf + (w * LPW + i) * 1024, vvo[i], (uint32_t)(t * TILE));
+  };
 
   const int q0 = qb * BM + w * 32;
   const int qrow = q0 + lr;
   const bool qvalid = qrow < S;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
+
+  // ---- KV tile counts ----
+  const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
+  const int nT = (int)((kv_end + BN - 1) / BN);
+  const int64_t wave_end = CAUSAL ? ((int64_t)q0 + 32 < S ? (int64_t)q0 + 32 : S) : S;
+  const int nTw = q0 < S ? (int)((wave_end + BN - 1) / BN) : 0;  // tiles with any unmasked key
+
+  // Start the first copies before the prologue's own global loads.
+  copy_k(0, K0);
+  copy_v(0, V0);
+  if (nT > 1) copy_k(1, K1);
 
   // ---- prologue: Q rows -> B operands (optionally RMSNorm + RoPE) ----
   bf16x8_t qreg[NC];
@@ -195,126 +280,131 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     }
   }
 
-  // ---- KV sweep ----
-  const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
-  const int nT = (int)((kv_end + BN - 1) / BN);
-  const int64_t wave_end = CAUSAL ? ((int64_t)q0 + 32 < S ? (int64_t)q0 + 32 : S) : S;
-  const int nTw = q0 < S ? (int)((wave_end + BN - 1) / BN) : 0;  // tiles with any unmasked key
+  // ---- LDS read addressing (constant per lane) ----
+  // GEMM1: lane reads row 32*kb + lr, chunk 2c + g; with the K swizzle the
+  // slot is 8*(c/4) + ((2*(c%4) + g) ^ (lr & 7)).
+  uint32_t kra[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kra[j] = (uint32_t)(lr * RB + (((2 * j + g) ^ (lr & 7)) << 4));
+  // GEMM2 transpose reads: 16-lane group supplies rows (lane%16)/4 + 4g of a
+  // 16-key step and 4-column runs 16*((lane/16)%2) + 4*(lane%4) of a 32-wide
+  // d block; with the V swizzle the slot is 8*(db/2) + ((4*(db%2) + 2*hh + kk) ^ 2m).
+  uint32_t vra[2];
+  {
+    const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
+    const int row0 = ((lane & 15) >> 2) + 4 * g;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) vra[e] = (uint32_t)(row0 * RB + (((4 * e + 2 * hh + kk) ^ (2 * m)) << 4) + (lane & 1) * 8);
+  }
 
   f32x16_t o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
-  float m_run = -INFINITY;  // running max of logits (log2 domain)
+  float m_run = -INFINITY;  // reference max of logits (log2 domain)
   float l_run = 0.f;        // this lane's partial row sum
 
-  u32x4_t kpre[LDC], vpre[LDC];
-  auto gload = [&](int t) {
+  auto gemm1 = [&](f32x16_t (&s)[NKB], int kbuf) {
 #pragma unroll
-    for (int i = 0; i < LDC; ++i) {
-      const int e = tid + NT * i;
-      const int key = e / CPR, ch = e % CPR;
-      const int64_t kabs = (int64_t)t * BN + key;
-      const bool ok = kabs < S;
-      kpre[i] = ok ? ld16(kbase + kabs * D + 8 * ch) : zero;
-      vpre[i] = ok ? ld16(vbase + kabs * D + 8 * ch) : zero;
+    for (int kb = 0; kb < NKB; ++kb) {
+      s[kb] = f32x16_t{};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8_t a =
+            *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 3] + (c >> 2) * 128);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
+      }
     }
   };
 
-  // transpose-read addressing (constant per lane): 16-lane group gg supplies
-  // rows key0 + (lane%16)/4, columns 16*(gg&1) + 4*(lane%4) of a 32-wide d block
-  const int tr_r = lane & 15, tr_gg = lane >> 4;
-  const int tr_row = (tr_r >> 2) + 4 * g;
-  const int tr_col = 16 * (tr_gg & 1) + 4 * (tr_r & 3);
-
-  gload(0);
-  for (int t = 0; t < nT; ++t) {
-#pragma unroll
-    for (int i = 0; i < LDC; ++i) {
-      const int e = tid + NT * i;
-      const int key = e / CPR, ch = e % CPR;
-      st16(&Ks[key * KST + 8 * ch], kpre[i]);
-      st16(&Vs[key * VST + 8 * ch], vpre[i]);
-    }
-    __syncthreads();
-    if (t + 1 < nT) gload(t + 1);
-
-    if (t < nTw) {  // wave-uniform
-      // GEMM1: S^T[key][query] for BN keys x 32 queries
-      f32x16_t s[NKB];
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        s[kb] = f32x16_t{};
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(&Ks[(32 * kb + lr) * KST + 16 * c + 8 * g]);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
-        }
-      }
-      // masks: register i of block kb holds key 32*kb + 8*(i/4) + 4*g + i%4
-      const int64_t kt = (int64_t)t * BN;
-      const bool need_mask = (CAUSAL && kt + BN - 1 > q0) || (kt + BN > S);
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int64_t key = kt + 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-            if ((CAUSAL && key > qrow) || key >= S) s[kb][i] = -INFINITY;
-          }
-      }
-      // online softmax (log2 domain)
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-      mx = max_halves(mx);
-      const float m_new = fmaxf(m_run, mx * cl);
-      if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
-        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-        m_run = m_new;
-      }
-      const float neg_m = -m_run;
-      float lsum = 0.f;
+  auto softmax_pv = [&](f32x16_t (&s)[NKB], int t, int vbuf) {
+    // masks: register i of block kb holds key 32*kb + 8*(i/4) + 4*g + i%4
+    const int64_t kt = (int64_t)t * BN;
+    const bool need_mask = (CAUSAL && kt + BN - 1 > q0) || (kt + BN > S);
+    if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], cl, neg_m));
-          s[kb][i] = pv;
-          lsum += pv;
+          const int64_t key = kt + 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
+          if ((CAUSAL && key > qrow) || key >= S) s[kb][i] = -INFINITY;
         }
-      l_run += lsum;
-      // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
-      bf16x8_t pb[NK16];
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int c2 = 0; c2 < NK16; ++c2) {
-        u32x4_t wv;
+    for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          wv[j] = pack_bf16x2(s[c2 >> 1][8 * (c2 & 1) + 2 * j], s[c2 >> 1][8 * (c2 & 1) + 2 * j + 1]);
-        pb[c2] = as_bf16x8(wv);
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
+    mx = max_halves(mx) * cl;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_SLACK) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+      m_run = m_new;
+    }
+    const float neg_m = -m_run;
+    float lsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], cl, neg_m));
+        s[kb][i] = pv;
+        lsum += pv;
       }
-      // GEMM2: O^T[d][query] += V^T . P^T; the A operand's slot j of half g is
-      // key 16*c2 + 8*(j/4) + 4*g + j%4, matching the P^T registers above.
+    l_run += lsum;
+    // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
+    bf16x8_t pb[NK16];
 #pragma unroll
-      for (int c2 = 0; c2 < NK16; ++c2) {
+    for (int c2 = 0; c2 < NK16; ++c2) {
+      u32x4_t wv;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint16_t *base = &Vs[(16 * c2 + tr_row) * VST + 32 * db + tr_col];
-          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
-          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * VST));
-          const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
-        }
+      for (int j = 0; j < 4; ++j)
+        wv[j] = pack_bf16x2(s[c2 >> 1][8 * (c2 & 1) + 2 * j], s[c2 >> 1][8 * (c2 & 1) + 2 * j + 1]);
+      pb[c2] = as_bf16x8(wv);
+    }
+    // GEMM2: O^T[d][query] += V^T . P^T; the A operand's slot j of half g is
+    // key 16*c2 + 8*(j/4) + 4*g + j%4, matching the P^T registers above.
+#pragma unroll
+    for (int c2 = 0; c2 < NK16; ++c2) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 1] + (db >> 1) * 128;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
       }
     }
+  };
+
+  // One pipelined iteration; PAR = t % 2 selects the buffers at compile time.
+  auto iteration = [&](auto par, int t, f32x16_t (&cur)[NKB], f32x16_t (&nxt)[NKB]) {
+    constexpr int PAR = decltype(par)::value;
+    constexpr int KNEXT = PAR ? K0 : K1;   // holds K(t+1)
+    constexpr int KFREE = PAR ? K1 : K0;   // held K(t), read in the previous iteration
+    constexpr int VCUR = PAR ? V1 : V0;    // holds V(t)
+    constexpr int VFREE = PAR ? V0 : V1;   // held V(t-1)
+    wait_copies();
     __syncthreads();
+    if (t + 2 < nT) copy_k(t + 2, KFREE);
+    if (t + 1 < nT) copy_v(t + 1, VFREE);
+    if (t + 1 < nTw) gemm1(nxt, KNEXT);
+    if (t < nTw) softmax_pv(cur, t, VCUR);
+  };
+
+  f32x16_t sa[NKB], sb[NKB];
+  wait_copies();
+  __syncthreads();
+  if (nTw > 0) gemm1(sa, K0);
+  for (int t = 0;;) {
+    iteration(std::integral_constant<int, 0>{}, t, sa, sb);
+    if (++t >= nT) break;
+    iteration(std::integral_constant<int, 1>{}, t, sb, sa);
+    if (++t >= nT) break;
   }
 
   // ---- epilogue: O = O^T / l, BF16 rows ----
