@@ -29,6 +29,12 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(INCL
           "-Wall", "-Wno-unused-function"]
 
 
+# Per-file flags.  attention.hip: no NaN inputs reach its max reductions
+# (masked scores are -inf, not NaN), and without NaN semantics fmaxf needs no
+# canonicalising instructions, so max trees map onto v_max3_f32.
+FILE_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -57,12 +63,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     objs = [objdir / (s.stem + ".o") for s in sources]
-    cmds = [[cc, *COMMON, *DEVICE_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objs)]
+    cmds = [[cc, *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(s.name, []), "-c", str(s), "-o", str(o)]
+            for s, o in zip(sources, objs)]
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    # -z defs: an unresolved symbol (e.g. a kernel stub the host pass did not
+    # emit) fails the build instead of the first dlopen.
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

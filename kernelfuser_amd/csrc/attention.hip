@@ -3,12 +3,23 @@
 // (src/e1_rope_publication_v1.py:608-649) and factored_attention_kernel
 // (src/e1_qk_publication_v3.py:612-638).
 //
-// Work decomposition: one workgroup = 4 waves = BM=128 query rows of one
-// (batch, Q head); each wave owns 32 query rows for the whole KV sweep.
+// Two kernels share the arithmetic below:
+//   attn_pp_kernel   D=128, Hq/Hkv even (the Qwen3 shapes).  One workgroup =
+//                    8 waves = two Q heads of one GQA group x 128 query rows.
+//                    Waves w and w+4 run on the same SIMD; group A (waves 0-3,
+//                    first head) and group B (waves 4-7, second head) alternate
+//                    phase by phase between an MFMA phase (GEMM1 of tile t and
+//                    GEMM2 of tile t-1) and a VALU phase (softmax of tile t),
+//                    so on every SIMD one wave keeps the matrix core busy while
+//                    the other computes exponentials.  Each K/V tile staged in
+//                    LDS serves both heads.
+//   attn_fwd_kernel  any D in {128, 256} and GQA ratio: 4 waves = 128 query
+//                    rows of one head; GEMM1 of tile t+1 is issued ahead of the
+//                    softmax and GEMM2 of tile t.
 //
 // Transposed formulation (everything stays in registers between the GEMMs):
 //   GEMM1  S^T = K . Q^T   A = K tile rows from LDS (ds_read_b128),
-//                           B = the wave's Q rows, held in VGPRs as MFMA
+//                           B = the wave's 32 Q rows, held in VGPRs as MFMA
 //                               B-operands for the whole sweep;
 //          the 32x32 accumulator gives every lane ONE query (lane % 32) and 16
 //          keys, so the row max / row sum are lane-local plus one
@@ -23,17 +34,13 @@
 // C[m][n] -> lane n + 32*((m/4)%2), register (m/8)*4 + m%4.
 //
 // K/V staging: tiles of BN rows (16 KiB each) are copied HBM -> LDS by the
-// buffer unit (buffer_load_dwordx4 ... lds: lane L of a load writes LDS bytes
+// buffer unit (buffer_load_dwordx4 ... lds: lane L of a copy writes LDS bytes
 // base + 16*L), so no VGPRs, no ds_write and no bounds branches are spent on
 // staging: rows past S lie outside the buffer descriptor's range and arrive as
 // zeros.  Both K and V are double-buffered; the 16-byte chunks of each row are
-// XOR-swizzled (K: chunk ^ (row & 7); V: chunk ^ 2*(row & 3)) so the GEMM1
-// row reads and the GEMM2 transpose reads are bank-conflict free.
-//
-// Pipeline (one barrier per KV tile): iteration t issues the copies of K(t+2)
-// and V(t+1), then GEMM1 of tile t+1 and the softmax + GEMM2 of tile t, so the
-// exp2/max/sum VALU work of tile t overlaps the MFMAs of tile t+1 and each
-// copy has a full iteration to land.
+// XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 4*(row & 3)) so that the 16
+// lanes of a GEMM1 row read (16 B each) and the 32 lanes of a GEMM2 transpose
+// read (8 B each) cover all 64 LDS banks exactly once.
 //
 // Q prologue (query fusion): the wave's raw Q rows are loaded straight into
 // the B-operand layout (lane: row lane%32, columns 16c + 8*(lane/32) + 0..7),
@@ -47,9 +54,8 @@
 // 256, far inside FP32/BF16 range, and O is rescaled a handful of times per
 // row instead of on every tile; after the final division by the row sum the
 // result is the same softmax.  Causal: the KV loop stops at the diagonal,
-// masks are applied only on diagonal/tail tiles, waves skip tiles that are
-// fully masked for their rows, and the grid issues the longest query blocks
-// first.
+// masks are applied only on diagonal/tail tiles, and the grid issues the
+// longest query blocks first.
 #include <math.h>
 
 #include "kfmi_device.h"
@@ -102,7 +108,7 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t bytes)
 
 // 16 bytes per lane from buffer offset voff + soff into LDS at lds + 16*lane.
 // Issued as inline assembly so the compiler does not guard every later LDS
-// read with a wait for it; the kernel orders copies and reads itself
+// read with a wait for it; the kernels order copies and reads themselves
 // (wait_copies + barrier).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; it is set right here
@@ -119,6 +125,553 @@ __device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: probabilities stay <= 2^8
 
+// Phase fences: an empty volatile asm that takes the phase's results as
+// inputs, so the compiler finishes computing them before the barrier that
+// ends the phase instead of sinking that work into the next phase.
+// (The asm operands only exist in the device pass; the host pass of this
+// file never executes device code.)
+template <int N>
+__device__ __forceinline__ void fence_regs(const f32x16_t (&x)[N]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" ::"v"(x[i]));
+#endif
+}
+template <int N>
+__device__ __forceinline__ void fence_regs(const bf16x8_t (&x)[N]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" ::"v"(x[i]));
+#endif
+}
+__device__ __forceinline__ void fence_regs(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" ::"v"(x));
+#endif
+}
+// Phase entry: the registers count as rewritten here, so no work that reads
+// them is hoisted above the barrier that starts the phase.
+template <int N>
+__device__ __forceinline__ void fence_in(f32x16_t (&x)[N]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
+#endif
+}
+template <int N>
+__device__ __forceinline__ void fence_in(bf16x8_t (&x)[N]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(x[i]));
+#endif
+}
+
+// Source offset (bytes, within the head's rows) of the chunk that copy `inst`
+// places in LDS slot lane%CPR of row inst*RPI + lane/CPR, for the K or V
+// swizzle.  The copy's own row offset inst*1024 is added as soffset.
+template <int D>
+__device__ __forceinline__ uint32_t copy_lane_offset(int inst, int lane, bool v_tile) {
+  constexpr int RB = 2 * D, CPR = D / 8, RPI = 1024 / RB;
+  const int row = inst * RPI + lane / CPR;
+  const int slot = lane % CPR;
+  const int chunk = v_tile ? (slot ^ ((row & 3) << 2)) : (slot ^ (row & 15));
+  return (uint32_t)((lane / CPR) * RB + (chunk << 4));
+}
+
+// Per-lane LDS read offsets.  GEMM1: lane reads row 32*kb + lr, chunk 2c + g;
+// with the K swizzle the slot is 16*(c/8) + ((2*(c%8) + g) ^ (lr & 15)), so
+// kra[c%8] + 256*(c/8).  GEMM2 transpose reads: the 16-lane group supplies rows
+// (lane%16)/4 + 4g of a 16-key step and 4-column runs 16*((lane/16)%2) +
+// 4*(lane%4) of a 32-wide d block, i.e. chunk 4*db + 2*hh + kk; with the V
+// swizzle (row % 4 = m) the slot is 16*(db/4) + 4*((db%4) ^ m) + 2*hh + kk, so
+// vra[db%4] + 256*(db/4).
+template <int D>
+__device__ __forceinline__ void lds_read_offsets(int lane, uint32_t (&kra)[8], uint32_t (&vra)[4]) {
+  constexpr int RB = 2 * D;
+  const int g = lane >> 5, lr = lane & 31;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kra[j] = (uint32_t)(lr * RB + (((2 * j + g) ^ (lr & 15)) << 4));
+  const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
+  const int row0 = ((lane & 15) >> 2) + 4 * g;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) vra[e] = (uint32_t)(row0 * RB + ((4 * (e ^ m) + 2 * hh + kk) << 4) + (lane & 1) * 8);
+}
+
+// Q prologue: the lane's query row -> GEMM1 B operands (columns 16c + 8g ..
+// +7), optionally RMSNorm * gamma (+ RoPE), and the lane's logit multiplier.
+// FOLD (FP32 style with a norm prologue only): the logit multiplier is
+// applied to the normalised FP32 row before its single rounding, so the MFMA
+// yields scores already in log2 units and cl becomes 1.
+template <int D, int PRO, int ST, bool FOLD = false>
+__device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, int qrow, bool qvalid, int g,
+                                           bf16x8_t (&qreg)[D / 16], float &cl) {
+  constexpr int NC = D / 16;
+  const uint16_t *qbase = p.q + qoff * D;
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+  cl = p.c_scale;
+  u32x4_t raw[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) raw[c] = qvalid ? ld16(qbase + (int64_t)qrow * D + 16 * c + 8 * g) : zero;
+  if constexpr (PRO == PRO_NONE) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
+  } else if constexpr (PRO == PRO_FACTORED_READ) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
+    cl = (qvalid ? p.inv[qoff + qrow] : 1.0f) * p.c_scale;  // qk:621
+  } else {
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8];
+      unpack8(raw[c], x);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
+    }
+    ss = sum_halves(ss);
+    const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+    if constexpr (PRO == PRO_FACTORED_CALC) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
+      if (p.inv != nullptr && g == 0 && qvalid) p.inv[qoff + qrow] = inv;  // qk:597-601
+      cl = inv * p.c_scale;                                              // qk:621
+    } else {
+      constexpr int HC = NC / 2;  // chunk c pairs with c ^ HC (columns d, d + D/2)
+#pragma unroll
+      for (int c = 0; c < HC; ++c) {
+        const int c2 = c + HC;
+        float x1[8], x2[8], g1[8], g2[8], n1[8], n2[8], y1[8], y2[8];
+        unpack8(raw[c], x1);
+        unpack8(raw[c2], x2);
+        unpack8(ld16(p.gq + 16 * c + 8 * g), g1);
+        unpack8(ld16(p.gq + 16 * c2 + 8 * g), g2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          n1[j] = norm_elem<ST>(x1[j], inv, g1[j]);
+          n2[j] = norm_elem<ST>(x2[j], inv, g2[j]);
+        }
+        if constexpr (PRO == PRO_NORM_ROPE) {
+          float cs1[8], sn1[8], cs2[8], sn2[8];
+          const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
+          unpack8(ld16(p.cos + trow + 16 * c + 8 * g), cs1);
+          unpack8(ld16(p.sin + trow + 16 * c + 8 * g), sn1);
+          unpack8(ld16(p.cos + trow + 16 * c2 + 8 * g), cs2);
+          unpack8(ld16(p.sin + trow + 16 * c2 + 8 * g), sn2);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            y1[j] = rope_elem<ST>(n1[j], n2[j], cs1[j], sn1[j], true);
+            y2[j] = rope_elem<ST>(n2[j], n1[j], cs2[j], sn2[j], false);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) { y1[j] = n1[j]; y2[j] = n2[j]; }
+        }
+        if constexpr (FOLD) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) { y1[j] = __fmul_rn(y1[j], p.c_scale); y2[j] = __fmul_rn(y2[j], p.c_scale); }
+        }
+        qreg[c] = as_bf16x8(pack8(y1));
+        qreg[c2] = as_bf16x8(pack8(y2));
+      }
+      if constexpr (FOLD) cl = 1.0f;
+    }
+  }
+}
+
+// Online-softmax state of one wave (32 query rows, one per lane pair).
+//   FOLD = false: scores s are raw q.k; logits = s*cl (one FMA per score).
+//   FOLD = true : GEMM1 starts from -m_run, so s already is logit - m_run
+//                 (Q carries the multiplier); one exp2 per score.  m_run starts
+//                 at 0 and the first tile always sets it to the exact row max.
+template <int D, int BN, bool CAUSAL, bool FOLD = false>
+struct Softmax {
+  static constexpr int NKB = BN / 32, NK16 = BN / 16, NDB = D / 32;
+  float m_run = FOLD ? 0.f : -INFINITY;  // reference max of logits (log2 domain)
+  float l_run = 0.f;                     // this lane's partial row sum
+  bool started = false;                  // FOLD: a tile has set m_run
+
+  // GEMM1 accumulator start value of this lane (FOLD: -m_run).
+  __device__ __forceinline__ float acc_init() const { return FOLD ? -m_run : 0.f; }
+
+  // Scores of KV tile t (keys t*BN ..) -> P^T operands pb; rescales o when
+  // the reference max has to move.
+  __device__ __forceinline__ void step(f32x16_t (&s)[NKB], int t, int q0, int qrow, int64_t S, int g, float cl,
+                                       f32x16_t (&o)[NDB], bf16x8_t (&pb)[NK16]) {
+    // masks: register i of block kb holds key kt + 4*g + c_i with the
+    // compile-time c_i = 32*kb + 8*(i/4) + i%4; a key is masked when it lies
+    // past the lane's query (causal) or past the sequence, i.e. when
+    // c_i > lim = min(qrow, S - 1) - kt - 4*g.
+    const int kt = t * BN;
+    const bool need_mask = (CAUSAL && kt + BN - 1 > q0) || (kt + BN > S);
+    if (need_mask) {
+      const int last = (int)(S - 1);
+      const int lim = (CAUSAL ? (qrow < last ? qrow : last) : last) - kt - 4 * g;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s[kb][i] = -INFINITY;
+    }
+    // Row max as a balanced tree (a serial chain would leave the VALU idle
+    // on dependency latency).
+    float mt[NKB * 8];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mt[kb * 8 + i] = fmaxf(s[kb][2 * i], s[kb][2 * i + 1]);
+#pragma unroll
+    for (int n = NKB * 4; n >= 1; n >>= 1)
+#pragma unroll
+      for (int i = 0; i < n; ++i) mt[i] = fmaxf(mt[i], mt[i + n]);
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};  // four interleaved partial sums
+    if constexpr (FOLD) {
+      const float mx = max_halves(mt[0]);  // tile max of logit - m_run
+      if (__builtin_amdgcn_ballot_w64(!started || mx > RESCALE_SLACK) != 0) {
+        // First tile: m_run := row max; later: raise m_run by the excess.
+        const float delta = started ? fmaxf(mx, 0.f) : mx;
+        const float alpha = started ? __builtin_amdgcn_exp2f(-delta) : 0.f;
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m_run += delta;
+        started = true;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kb][i] -= delta;
+      }
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(s[kb][i]);
+          s[kb][i] = pv;
+          ls[i & 3] += pv;
+        }
+    } else {
+      const float mx = max_halves(mt[0]) * cl;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_SLACK) != 0) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        m_run = m_new;
+      }
+      const float neg_m = -m_run;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], cl, neg_m));
+          s[kb][i] = pv;
+          ls[i & 3] += pv;
+        }
+    }
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
+#pragma unroll
+    for (int c2 = 0; c2 < NK16; ++c2) {
+      u32x4_t wv;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wv[j] = pack_bf16x2(s[c2 >> 1][8 * (c2 & 1) + 2 * j], s[c2 >> 1][8 * (c2 & 1) + 2 * j + 1]);
+      pb[c2] = as_bf16x8(wv);
+    }
+  }
+};
+
+// GEMM1: S^T (BN keys x 32 queries) of the K tile at LDS byte kbuf.
+template <int D, int BN>
+__device__ __forceinline__ void gemm1(const unsigned char *smem, int kbuf, const uint32_t (&kra)[8],
+                                      const bf16x8_t (&qreg)[D / 16], f32x16_t (&s)[BN / 32]) {
+  constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    s[kb] = f32x16_t{};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 7] + (c >> 3) * 256);
+      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
+    }
+  }
+  // Issue order: K reads run two MFMAs ahead (bounded register footprint).
+  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+  for (int i = 0; i < NKB * NC; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i + 2 < NKB * NC) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+  }
+}
+
+// GEMM2: O^T[d][query] += V^T . P^T for the V tile at LDS byte vbuf; the A
+// operand's slot j of half g is key 16*c2 + 8*(j/4) + 4*g + j%4, matching the
+// P^T registers of Softmax::step.
+template <int D, int BN>
+__device__ __forceinline__ void gemm2(const unsigned char *smem, int vbuf, const uint32_t (&vra)[4],
+                                      const bf16x8_t (&pb)[BN / 16], f32x16_t (&o)[D / 32]) {
+  constexpr int RB = 2 * D, NK16 = BN / 16, NDB = D / 32;
+#pragma unroll
+  for (int c2 = 0; c2 < NK16; ++c2) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 3] + (db >> 2) * 256;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
+    }
+  }
+  // Issue order: V^T reads (two per MFMA) run two MFMAs ahead.
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+  for (int i = 0; i < NK16 * NDB; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (i + 2 < NK16 * NDB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
+}
+
+// GEMM1 of one tile and GEMM2 of the previous tile as one straight-line block
+// (the ping-pong kernel's MFMA phase).  Issue order: six reads ahead, one read
+// after each GEMM1 MFMA, two after each GEMM2 MFMA, so every MFMA's operand
+// was requested several MFMAs earlier.
+template <int D, int BN>
+__device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, int vbuf, const uint32_t (&kra)[8],
+                                           const uint32_t (&vra)[4], const bf16x8_t (&qreg)[D / 16], float s0,
+                                           f32x16_t (&s)[BN / 32], const bf16x8_t (&pb)[BN / 16],
+                                           f32x16_t (&o)[D / 32]) {
+  constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16, NK16 = BN / 16, NDB = D / 32;
+  constexpr int M1 = NKB * NC, M2 = NK16 * NDB, READS = M1 + 2 * M2, AHEAD = 6;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s[kb][i] = s0;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 7] + (c >> 3) * 256);
+      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int c2 = 0; c2 < NK16; ++c2) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 3] + (db >> 2) * 256;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
+    }
+  }
+  int issued = AHEAD;
+  __builtin_amdgcn_sched_group_barrier(0x100, AHEAD, 0);
+#pragma unroll
+  for (int i = 0; i < M1 + M2; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    const int want = i < M1 ? 1 : 2;
+    const int n = issued + want <= READS ? want : READS - issued;
+    if (n == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if (n == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    issued += n;
+  }
+}
+
+// Epilogue: O = O^T / l as BF16 rows.
+template <int D>
+__device__ __forceinline__ void store_rows(uint16_t *obase, int qrow, bool qvalid, int g, float l_run,
+                                           const f32x16_t (&o)[D / 32]) {
+  const float l_tot = sum_halves(l_run);
+  if (!qvalid) return;
+  const float rl = __fdiv_rn(1.0f, l_tot);
+  uint16_t *orow = obase + (int64_t)qrow * D;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      u32x2_t wv;
+      wv[0] = pack_bf16x2(o[db][4 * q4 + 0] * rl, o[db][4 * q4 + 1] * rl);
+      wv[1] = pack_bf16x2(o[db][4 * q4 + 2] * rl, o[db][4 * q4 + 3] * rl);
+      *reinterpret_cast<u32x2_t *>(orow + 32 * db + 8 * q4 + 4 * g) = wv;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Ping-pong kernel: D=128, BN=64, two Q heads of a GQA group per workgroup.
+// ---------------------------------------------------------------------------
+template <bool CAUSAL, int PRO, int ST>
+__global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
+  constexpr int D = 128, BN = 64, BM = 128;
+  constexpr int TILE = BN * 2 * D;      // 16 KiB
+  constexpr int LPW = TILE / 1024 / 8;  // copies per wave per tile (2)
+  constexpr int NC = D / 16, NDB = D / 32, NKB = BN / 32, NK16 = BN / 16;
+  constexpr int K0 = 0, K1 = TILE, V0 = 2 * TILE, V1 = 3 * TILE;
+
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
+  const int grp = w >> 2;  // 0: first head (group A), 1: second head (group B)
+  const int wq = w & 3;    // 32-row block of the workgroup's 128 rows
+  const int g = lane >> 5;
+  const int lr = lane & 31;
+  const int64_t S = p.S;
+
+  // ---- work item: (query block, KV head, head pair); heaviest blocks first;
+  // all head pairs of a KV head on one XCD so its K/V stay in that L2 ----
+  const int G = p.Hq / p.Hkv;
+  const int HP = G / 2;
+  const int npairs = p.B * p.Hkv * HP;
+  const int bid = blockIdx.x;
+  const int rank = bid / npairs;
+  const int r = bid - rank * npairs;
+  const int qb = CAUSAL ? p.n_qblocks - 1 - rank : rank;
+  int kvi, j;
+  if (p.xcd_remap) {
+    const int xcd = r & 7, jj = r >> 3;
+    kvi = xcd + 8 * (jj / HP);
+    j = jj % HP;
+  } else {
+    kvi = r / HP;
+    j = r - kvi * HP;
+  }
+  const int b = kvi / p.Hkv;
+  const int kvh = kvi - b * p.Hkv;
+  const int h = kvh * G + 2 * j + grp;
+  const int64_t qoff = ((int64_t)b * p.Hq + h) * S;
+  const int64_t kvoff = ((int64_t)b * p.Hkv + kvh) * S;
+
+  const uint32_t head_bytes = (uint32_t)(S * 2 * D);
+  const i32x4_t krs = buffer_rsrc(p.k + kvoff * D, head_bytes);
+  const i32x4_t vrs = buffer_rsrc(p.v + kvoff * D, head_bytes);
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
+  uint32_t kvo[LPW], vvo[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    kvo[i] = copy_lane_offset<D>(w * LPW + i, lane, false);
+    vvo[i] = copy_lane_offset<D>(w * LPW + i, lane, true);
+  }
+  auto copy_k = [&](int t, int buf) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int inst = w * LPW + i;
+      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i], (uint32_t)(t * TILE + inst * 1024));
+    }
+  };
+  auto copy_v = [&](int t, int buf) {
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int inst = w * LPW + i;
+      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], (uint32_t)(t * TILE + inst * 1024));
+    }
+  };
+
+  const int q0 = qb * BM + wq * 32;
+  const int qrow = q0 + lr;
+  const bool qvalid = qrow < S;
+  const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
+  const int nT = (int)((kv_end + BN - 1) / BN);
+
+  copy_k(0, K0);
+
+  constexpr bool FOLD = ST == ST_FP32 && (PRO == PRO_NORM || PRO == PRO_NORM_ROPE);
+  bf16x8_t qreg[NC];
+  float cl;
+  q_prologue<D, PRO, ST, FOLD>(p, qoff, qrow, qvalid, g, qreg, cl);
+
+  uint32_t kra[8], vra[4];
+  lds_read_offsets<D>(lane, kra, vra);
+
+  f32x16_t o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
+  Softmax<D, BN, CAUSAL, FOLD> sm;
+  f32x16_t s[NKB];
+  bf16x8_t pb[NK16];
+#pragma unroll
+  for (int c2 = 0; c2 < NK16; ++c2) pb[c2] = bf16x8_t{};
+  {
+    // Zero the V1 buffer read by M(0) (it is first filled in iteration 1).
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < TILE / (16 * 512); ++i) st16((uint16_t *)(smem + V1 + 16 * (tid + 512 * i)), z);
+  }
+
+  // Each wave runs M(0) V(0) M(1) V(1) ... V(nT-1) M(nT) with
+  //   M(t) = GEMM1 of tile t (t < nT) + GEMM2 of tile t-1 (t >= 1),
+  //   V(t) = softmax of tile t.
+  // Group B runs one phase behind group A, so every phase pairs an M with a
+  // V on each SIMD: iteration t = phase 2t (A: M(t), B: V(t-1)) and phase
+  // 2t+1 (A: V(t), B: M(t)).  K(t+1) and V(t) are copied at the start of
+  // phase 2t into the buffers that K(t-1) and V(t-2) left at the end of phase
+  // 2t-1, and waited for at the start of phase 2t+2.  Both groups pass the
+  // same two barriers per iteration; each group has its own straight-line
+  // loop, and PAR = t % 2 selects the buffers at compile time.
+  auto copies = [&](auto par, int t) {
+    constexpr int PAR = decltype(par)::value;
+    wait_copies();
+    __syncthreads();
+    if (t + 1 < nT) copy_k(t + 1, PAR ? K0 : K1);
+    if (t < nT) copy_v(t, PAR ? V1 : V0);
+  };
+  // M(0)'s GEMM2 multiplies the zero P^T operands with the zero-filled V1
+  // buffer and M(nT)'s GEMM1 reads a stale K buffer into scores nobody uses:
+  // the MFMA phase is one straight-line block, so its LDS reads can run ahead
+  // of the MFMAs that consume them across the GEMM1/GEMM2 boundary.
+  auto mphase = [&](auto par, int t) {
+    constexpr int PAR = decltype(par)::value;
+    fence_in(pb);
+    fence_in(o);
+    mfma_phase<D, BN>(smem, PAR ? K1 : K0, PAR ? V0 : V1, kra, vra, qreg, sm.acc_init(), s, pb, o);
+    fence_regs(s);
+    fence_regs(o);
+  };
+  auto vphase = [&](int t) {
+    fence_in(s);
+    fence_in(o);
+    sm.step(s, t, q0, qrow, S, g, cl, o, pb);
+    fence_regs(pb);
+    fence_regs(o);
+    fence_regs(sm.l_run);
+  };
+  if (grp == 0) {
+    auto iter = [&](auto par, int t) {
+      copies(par, t);
+      mphase(par, t);
+      __syncthreads();
+      if (t < nT) vphase(t);
+    };
+    for (int t = 0;;) {
+      iter(std::integral_constant<int, 0>{}, t);
+      if (++t > nT) break;
+      iter(std::integral_constant<int, 1>{}, t);
+      if (++t > nT) break;
+    }
+  } else {
+    auto iter = [&](auto par, int t) {
+      copies(par, t);
+      if (t >= 1) vphase(t - 1);
+      __syncthreads();
+      mphase(par, t);
+    };
+    for (int t = 0;;) {
+      iter(std::integral_constant<int, 0>{}, t);
+      if (++t > nT) break;
+      iter(std::integral_constant<int, 1>{}, t);
+      if (++t > nT) break;
+    }
+  }
+
+  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+}
+
+// ---------------------------------------------------------------------------
+// General kernel: one head, 4 waves x 32 rows, D in {128, 256}.
+// ---------------------------------------------------------------------------
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
 __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnParams p) {
   constexpr int BM = 128;            // query rows per workgroup (4 waves x 32)
@@ -126,12 +679,7 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   constexpr int TILE = BN * RB;      // bytes per K or V tile
   constexpr int NINST = TILE / 1024; // 1 KiB copies per tile
   constexpr int LPW = NINST / 4;     // copies per wave per tile
-  constexpr int RPI = 1024 / RB;     // rows per copy
-  constexpr int CPR = D / 8;         // 16-byte chunks per row
-  constexpr int NC = D / 16;         // GEMM1 k-steps (16 columns of d)
-  constexpr int NDB = D / 32;        // GEMM2 output blocks (32 columns of d)
-  constexpr int NKB = BN / 32;       // GEMM1 output blocks (32 keys)
-  constexpr int NK16 = BN / 16;      // GEMM2 k-steps (16 keys)
+  constexpr int NC = D / 16, NKB = BN / 32, NK16 = BN / 16, NDB = D / 32;
   constexpr int K0 = 0, K1 = TILE, V0 = 2 * TILE, V1 = 3 * TILE;
   static_assert(TILE == 16384 && LPW * 4 == NINST, "tiles are 16 KiB, 4 copies per wave");
 
@@ -156,10 +704,10 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     // Workgroups are dispatched round-robin over the 8 XCDs (bid % 8).  Map
     // KV group kg to XCD kg % 8 so the G query heads that read the same K/V
     // share one L2.
-    const int xcd = r & 7, j = r >> 3;
-    const int kg = xcd + 8 * (j / G);
+    const int xcd = r & 7, jj = r >> 3;
+    const int kg = xcd + 8 * (jj / G);
     b = kg / p.Hkv;
-    h = (kg - b * p.Hkv) * G + j % G;
+    h = (kg - b * p.Hkv) * G + jj % G;
   } else {
     b = r / p.Hq;
     h = r - b * p.Hq;
@@ -167,39 +715,35 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   const int kvh = h / G;
   const int64_t qoff = ((int64_t)b * p.Hq + h) * S;
   const int64_t kvoff = ((int64_t)b * p.Hkv + kvh) * S;
-  const uint16_t *qbase = p.q + qoff * D;
-  uint16_t *obase = p.out + qoff * D;
 
-  // Buffer descriptors of this head's K and V rows: reads at or past row S
-  // return zeros.
   const uint32_t head_bytes = (uint32_t)(S * RB);
   const i32x4_t krs = buffer_rsrc(p.k + kvoff * D, head_bytes);
   const i32x4_t vrs = buffer_rsrc(p.v + kvoff * D, head_bytes);
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
-
-  // Copy addressing: copy i of this wave fills LDS rows (w*LPW+i)*RPI + lane/CPR,
-  // slot lane%CPR, with the source chunk that the swizzle places there.
   uint32_t kvo[LPW], vvo[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
-    const int row = (w * LPW + i) * RPI + lane / CPR;
-    const int slot = lane % CPR;
-    kvo[i] = (uint32_t)(row * RB + ((slot ^ (row & 7)) << 4));
-    vvo[i] = (uint32_t)(row * RB + ((slot ^ ((row & 3) << 1)) << 4));
+    kvo[i] = copy_lane_offset<D>(w * LPW + i, lane, false);
+    vvo[i] = copy_lane_offset<D>(w * LPW + i, lane, true);
   }
   auto copy_k = [&](int t, int buf) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) copy16_to_lds(krs, lds0 + buf + (w * LPW + i) * 1024, kvo[i], (uint32_t)(t * TILE));
+    for (int i = 0; i < LPW; ++i) {
+      const int inst = w * LPW + i;
+      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i], (uint32_t)(t * TILE + inst * 1024));
+    }
   };
   auto copy_v = [&](int t, int buf) {
 #pragma unroll
-    for (int i = 0; i < LPW; ++i) copy16_to_lds(vrs, lds0 + buf + (w * LPW + i) * 1024, vvo[i], (uint32_t)(t * TILE));
+    for (int i = 0; i < LPW; ++i) {
+      const int inst = w * LPW + i;
+      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], (uint32_t)(t * TILE + inst * 1024));
+    }
   };
 
   const int q0 = qb * BM + w * 32;
   const int qrow = q0 + lr;
   const bool qvalid = qrow < S;
-  const u32x4_t zero = {0u, 0u, 0u, 0u};
 
   // ---- KV tile counts ----
   const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
@@ -212,176 +756,21 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   copy_v(0, V0);
   if (nT > 1) copy_k(1, K1);
 
-  // ---- prologue: Q rows -> B operands (optionally RMSNorm + RoPE) ----
   bf16x8_t qreg[NC];
-  float cl = p.c_scale;  // logit multiplier of this lane's query row
-  {
-    u32x4_t raw[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) raw[c] = qvalid ? ld16(qbase + (int64_t)qrow * D + 16 * c + 8 * g) : zero;
-    if constexpr (PRO == PRO_NONE) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
-    } else if constexpr (PRO == PRO_FACTORED_READ) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
-      cl = (qvalid ? p.inv[qoff + qrow] : 1.0f) * p.c_scale;  // qk:621
-    } else {
-      float ss = 0.f;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        float x[8];
-        unpack8(raw[c], x);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
-      }
-      ss = sum_halves(ss);
-      const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
-      if constexpr (PRO == PRO_FACTORED_CALC) {
-#pragma unroll
-        for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
-        if (p.inv != nullptr && g == 0 && qvalid) p.inv[qoff + qrow] = inv;  // qk:597-601
-        cl = inv * p.c_scale;                                              // qk:621
-      } else {
-        constexpr int HC = NC / 2;  // chunk c pairs with c ^ HC (columns d, d + D/2)
-#pragma unroll
-        for (int c = 0; c < HC; ++c) {
-          const int c2 = c + HC;
-          float x1[8], x2[8], g1[8], g2[8], n1[8], n2[8], y1[8], y2[8];
-          unpack8(raw[c], x1);
-          unpack8(raw[c2], x2);
-          unpack8(ld16(p.gq + 16 * c + 8 * g), g1);
-          unpack8(ld16(p.gq + 16 * c2 + 8 * g), g2);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            n1[j] = norm_elem<ST>(x1[j], inv, g1[j]);
-            n2[j] = norm_elem<ST>(x2[j], inv, g2[j]);
-          }
-          if constexpr (PRO == PRO_NORM_ROPE) {
-            float cs1[8], sn1[8], cs2[8], sn2[8];
-            const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
-            unpack8(ld16(p.cos + trow + 16 * c + 8 * g), cs1);
-            unpack8(ld16(p.sin + trow + 16 * c + 8 * g), sn1);
-            unpack8(ld16(p.cos + trow + 16 * c2 + 8 * g), cs2);
-            unpack8(ld16(p.sin + trow + 16 * c2 + 8 * g), sn2);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              y1[j] = rope_elem<ST>(n1[j], n2[j], cs1[j], sn1[j], true);
-              y2[j] = rope_elem<ST>(n2[j], n1[j], cs2[j], sn2[j], false);
-            }
-          } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) { y1[j] = n1[j]; y2[j] = n2[j]; }
-          }
-          qreg[c] = as_bf16x8(pack8(y1));
-          qreg[c2] = as_bf16x8(pack8(y2));
-        }
-      }
-    }
-  }
+  float cl;
+  q_prologue<D, PRO, ST>(p, qoff, qrow, qvalid, g, qreg, cl);
 
-  // ---- LDS read addressing (constant per lane) ----
-  // GEMM1: lane reads row 32*kb + lr, chunk 2c + g; with the K swizzle the
-  // slot is 8*(c/4) + ((2*(c%4) + g) ^ (lr & 7)).
-  uint32_t kra[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) kra[j] = (uint32_t)(lr * RB + (((2 * j + g) ^ (lr & 7)) << 4));
-  // GEMM2 transpose reads: 16-lane group supplies rows (lane%16)/4 + 4g of a
-  // 16-key step and 4-column runs 16*((lane/16)%2) + 4*(lane%4) of a 32-wide
-  // d block; with the V swizzle the slot is 8*(db/2) + ((4*(db%2) + 2*hh + kk) ^ 2m).
-  uint32_t vra[2];
-  {
-    const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
-    const int row0 = ((lane & 15) >> 2) + 4 * g;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) vra[e] = (uint32_t)(row0 * RB + (((4 * e + 2 * hh + kk) ^ (2 * m)) << 4) + (lane & 1) * 8);
-  }
+  uint32_t kra[8], vra[4];
+  lds_read_offsets<D>(lane, kra, vra);
 
   f32x16_t o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
-  float m_run = -INFINITY;  // reference max of logits (log2 domain)
-  float l_run = 0.f;        // this lane's partial row sum
+  Softmax<D, BN, CAUSAL> sm;
 
-  auto gemm1 = [&](f32x16_t (&s)[NKB], int kbuf) {
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      s[kb] = f32x16_t{};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const bf16x8_t a =
-            *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 3] + (c >> 2) * 128);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
-      }
-    }
-  };
-
-  auto softmax_pv = [&](f32x16_t (&s)[NKB], int t, int vbuf) {
-    // masks: register i of block kb holds key 32*kb + 8*(i/4) + 4*g + i%4
-    const int64_t kt = (int64_t)t * BN;
-    const bool need_mask = (CAUSAL && kt + BN - 1 > q0) || (kt + BN > S);
-    if (need_mask) {
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int64_t key = kt + 32 * kb + 8 * (i >> 2) + 4 * g + (i & 3);
-          if ((CAUSAL && key > qrow) || key >= S) s[kb][i] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kb][i]);
-    mx = max_halves(mx) * cl;
-    if (__builtin_amdgcn_ballot_w64(mx > m_run + RESCALE_SLACK) != 0) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-      m_run = m_new;
-    }
-    const float neg_m = -m_run;
-    float lsum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], cl, neg_m));
-        s[kb][i] = pv;
-        lsum += pv;
-      }
-    l_run += lsum;
-    // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
-    bf16x8_t pb[NK16];
-#pragma unroll
-    for (int c2 = 0; c2 < NK16; ++c2) {
-      u32x4_t wv;
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wv[j] = pack_bf16x2(s[c2 >> 1][8 * (c2 & 1) + 2 * j], s[c2 >> 1][8 * (c2 & 1) + 2 * j + 1]);
-      pb[c2] = as_bf16x8(wv);
-    }
-    // GEMM2: O^T[d][query] += V^T . P^T; the A operand's slot j of half g is
-    // key 16*c2 + 8*(j/4) + 4*g + j%4, matching the P^T registers above.
-#pragma unroll
-    for (int c2 = 0; c2 < NK16; ++c2) {
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 1] + (db >> 1) * 128;
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
-      }
-    }
-  };
-
-  // One pipelined iteration; PAR = t % 2 selects the buffers at compile time.
+  // Pipeline (one barrier per KV tile): iteration t issues the copies of
+  // K(t+2) and V(t+1), then GEMM1 of tile t+1 and the softmax + GEMM2 of tile
+  // t; each copy has a full iteration to land.  PAR = t % 2 selects buffers.
   auto iteration = [&](auto par, int t, f32x16_t (&cur)[NKB], f32x16_t (&nxt)[NKB]) {
     constexpr int PAR = decltype(par)::value;
     constexpr int KNEXT = PAR ? K0 : K1;   // holds K(t+1)
@@ -392,14 +781,18 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     __syncthreads();
     if (t + 2 < nT) copy_k(t + 2, KFREE);
     if (t + 1 < nT) copy_v(t + 1, VFREE);
-    if (t + 1 < nTw) gemm1(nxt, KNEXT);
-    if (t < nTw) softmax_pv(cur, t, VCUR);
+    if (t + 1 < nTw) gemm1<D, BN>(smem, KNEXT, kra, qreg, nxt);
+    if (t < nTw) {
+      bf16x8_t pb[NK16];
+      sm.step(cur, t, q0, qrow, S, g, cl, o, pb);
+      gemm2<D, BN>(smem, VCUR, vra, pb, o);
+    }
   };
 
   f32x16_t sa[NKB], sb[NKB];
   wait_copies();
   __syncthreads();
-  if (nTw > 0) gemm1(sa, K0);
+  if (nTw > 0) gemm1<D, BN>(smem, K0, kra, qreg, sa);
   for (int t = 0;;) {
     iteration(std::integral_constant<int, 0>{}, t, sa, sb);
     if (++t >= nT) break;
@@ -407,43 +800,35 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     if (++t >= nT) break;
   }
 
-  // ---- epilogue: O = O^T / l, BF16 rows ----
-  const float l_tot = sum_halves(l_run);
-  if (qvalid) {
-    const float rl = __fdiv_rn(1.0f, l_tot);
-    uint16_t *orow = obase + (int64_t)qrow * D;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        u32x2_t wv;
-        wv[0] = pack_bf16x2(o[db][4 * q4 + 0] * rl, o[db][4 * q4 + 1] * rl);
-        wv[1] = pack_bf16x2(o[db][4 * q4 + 2] * rl, o[db][4 * q4 + 3] * rl);
-        *reinterpret_cast<u32x2_t *>(orow + 32 * db + 8 * q4 + 4 * g) = wv;
-      }
-  }
+  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
 }
 
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
-hipError_t launch_t(const AttnParams &p, int blocks, hipStream_t s) {
+hipError_t launch_t(const AttnParams &p, bool pp, int blocks, hipStream_t s) {
+  if constexpr (D == 128) {
+    if (pp) {
+      hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST>), dim3(blocks), dim3(512), 0, s, p);
+      return hipGetLastError();
+    }
+  }
   hipLaunchKernelGGL((attn_fwd_kernel<D, BN, CAUSAL, PRO, ST>), dim3(blocks), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
 template <int D, int BN, bool CAUSAL>
-hipError_t dispatch_pro(const AttnParams &p, int pro, int st, int blocks, hipStream_t s) {
+hipError_t dispatch_pro(const AttnParams &p, int pro, int st, bool pp, int blocks, hipStream_t s) {
   switch (pro) {
-    case PRO_NONE: return launch_t<D, BN, CAUSAL, PRO_NONE, ST_FP32>(p, blocks, s);
-    case PRO_FACTORED_READ: return launch_t<D, BN, CAUSAL, PRO_FACTORED_READ, ST_FP32>(p, blocks, s);
-    case PRO_FACTORED_CALC: return launch_t<D, BN, CAUSAL, PRO_FACTORED_CALC, ST_FP32>(p, blocks, s);
+    case PRO_NONE: return launch_t<D, BN, CAUSAL, PRO_NONE, ST_FP32>(p, pp, blocks, s);
+    case PRO_FACTORED_READ: return launch_t<D, BN, CAUSAL, PRO_FACTORED_READ, ST_FP32>(p, pp, blocks, s);
+    case PRO_FACTORED_CALC: return launch_t<D, BN, CAUSAL, PRO_FACTORED_CALC, ST_FP32>(p, pp, blocks, s);
     case PRO_NORM:
-      if (st == ST_HF) return launch_t<D, BN, CAUSAL, PRO_NORM, ST_HF>(p, blocks, s);
-      if (st == ST_LEGACY) return launch_t<D, BN, CAUSAL, PRO_NORM, ST_LEGACY>(p, blocks, s);
-      return launch_t<D, BN, CAUSAL, PRO_NORM, ST_FP32>(p, blocks, s);
+      if (st == ST_HF) return launch_t<D, BN, CAUSAL, PRO_NORM, ST_HF>(p, pp, blocks, s);
+      if (st == ST_LEGACY) return launch_t<D, BN, CAUSAL, PRO_NORM, ST_LEGACY>(p, pp, blocks, s);
+      return launch_t<D, BN, CAUSAL, PRO_NORM, ST_FP32>(p, pp, blocks, s);
     case PRO_NORM_ROPE:
-      if (st == ST_HF) return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_HF>(p, blocks, s);
-      if (st == ST_LEGACY) return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_LEGACY>(p, blocks, s);
-      return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_FP32>(p, blocks, s);
+      if (st == ST_HF) return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_HF>(p, pp, blocks, s);
+      if (st == ST_LEGACY) return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_LEGACY>(p, pp, blocks, s);
+      return launch_t<D, BN, CAUSAL, PRO_NORM_ROPE, ST_FP32>(p, pp, blocks, s);
   }
   return hipErrorInvalidValue;
 }
@@ -463,15 +848,24 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   p.c_scale = (float)((factored ? 1.0 / sqrt((double)a.D) : a.scale) * LOG2E);
   const int BM = 128;
   p.n_qblocks = (int)((a.S + BM - 1) / BM);
-  const int nbh = p.B * p.Hq;
-  p.xcd_remap = (nbh % 8 == 0 && (p.B * p.Hkv) % 8 == 0) ? 1 : 0;
-  const int blocks = p.n_qblocks * nbh;
-  if (a.D == 128) {
-    return a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, blocks, stream)
-                    : dispatch_pro<128, 64, false>(p, a.prologue, a.style, blocks, stream);
+  const int G = p.Hq / p.Hkv;
+  const bool pp = a.D == 128 && G % 2 == 0;
+  int blocks;
+  if (pp) {
+    const int npairs = p.B * p.Hkv * (G / 2);
+    p.xcd_remap = ((p.B * p.Hkv) % 8 == 0 && npairs % 8 == 0) ? 1 : 0;
+    blocks = p.n_qblocks * npairs;
+  } else {
+    const int nbh = p.B * p.Hq;
+    p.xcd_remap = (nbh % 8 == 0 && (p.B * p.Hkv) % 8 == 0) ? 1 : 0;
+    blocks = p.n_qblocks * nbh;
   }
-  return a.causal ? dispatch_pro<256, 32, true>(p, a.prologue, a.style, blocks, stream)
-                  : dispatch_pro<256, 32, false>(p, a.prologue, a.style, blocks, stream);
+  if (a.D == 128) {
+    return a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, pp, blocks, stream)
+                    : dispatch_pro<128, 64, false>(p, a.prologue, a.style, pp, blocks, stream);
+  }
+  return a.causal ? dispatch_pro<256, 32, true>(p, a.prologue, a.style, false, blocks, stream)
+                  : dispatch_pro<256, 32, false>(p, a.prologue, a.style, false, blocks, stream);
 }
 
 }  // namespace kfmi
