@@ -102,8 +102,9 @@ def headline(args, torch, kf):
     xs = xs_cpu.to("cuda:0")
     out = torch.empty_like(xs.q)
     kn = torch.empty_like(xs.k)
+    vt = torch.empty_like(xs.v)  # V^T scratch: the preparation launch writes it
     step = lambda: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn,
-                                       norm_style=args.norm_style)
+                                       norm_style=args.norm_style, vt=vt)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -122,7 +123,8 @@ def headline(args, torch, kf):
            "tflops": flops / (ms_step * 1e-3) / 1e12}
     # The two kernels separately (events on the launch stream).
     attn_ms = time_launches(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
-                                                           causal=True, fuse_q=True, norm_style=args.norm_style),
+                                                           causal=True, fuse_q=True, norm_style=args.norm_style,
+                                                           vt=vt),
                             max(args.steps, 20))
     prep_ms = time_launches(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
                                                            norm_style=args.norm_style), max(args.steps, 20))

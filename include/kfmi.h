@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 1
+#define KFMI_ABI_VERSION 2
 
 /* status codes */
 #define KFMI_OK 0
@@ -78,24 +78,36 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *
  * k must be prepared (KN).  scale multiplies q.k (the reference uses D^-1/2,
  * rope:676).  bm is the number of query rows per workgroup (multiple of 32;
  * 128 is the tuned value), bn the key tile (64 or 128; a scheduling hint,
- * results do not depend on it). */
-int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *gq,
+ * results do not depend on it).  vt (optional, may be NULL): V transposed per
+ * head ([B,Hkv,D,S], as written by kfmi_transpose_v_bf16); used instead of v
+ * under the conditions given at kfmi_launch_attention_bf16. */
+int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *vt, const void *gq,
                         const void *cos, const void *sin, void *out,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                         double scale, float eps, int causal, int fuse_q, int norm_style,
                         int bm, int bn, void *stream);
 
-/* Both launches of launch_attention (rope:661-677): mode QUERY prepares K
+/* The launches of launch_attention (rope:661-677): mode QUERY prepares K
  * into kn (K rows only) then runs attention with the fused Q prologue; mode
  * UNFUSED prepares Q into qn and K into kn, then runs plain attention.  gk is
  * K's gamma.  Scratch kn (and qn for UNFUSED) is caller-allocated, as the
- * reference requires (rope:665-672).  cos/sin NULL disables RoPE. */
+ * reference requires (rope:665-672).  cos/sin NULL disables RoPE.
+ * vt (optional, may be NULL): caller-allocated scratch of V's size; when
+ * given and D == 128, Hq/Hkv is even and S % 8 == 0, the preparation launch
+ * also writes V transposed per head ([B,Hkv,D,S]) and the attention kernel
+ * reads that instead of V (one LDS read per V operand instead of two).
+ * Results are identical either way. */
 int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
                                const void *gq, const void *gk, const void *cos,
-                               const void *sin, void *out, void *qn, void *kn,
+                               const void *sin, void *out, void *qn, void *kn, void *vt,
                                int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                                double scale, float eps, int causal, int mode,
                                int norm_style, int bm, int bn, void *stream);
+
+/* vt[b,h,d,s] = v[b,h,s,d] for B*H heads of S rows of D (D 128 or 256,
+ * S % 8 == 0): the V^T scratch of kfmi_launch_attention_bf16, as a separate
+ * launch.  No counterpart in the reference (its kernels read V directly). */
+int kfmi_transpose_v_bf16(const void *v, void *vt, int64_t BH, int64_t S, int64_t D, void *stream);
 
 /* Factored no-RoPE preparation (qk:592-609): INV[B,Hq,S] = rsqrt(mean q^2 +
  * eps) (float32) for every Q row and KN = bf16(k * inv_k * gk * gq) for every

@@ -25,12 +25,14 @@ from .ops import (  # noqa: F401
     optimized_attention,
     prepare_attention,
     prepare_factored,
+    transpose_v,
+    uses_vt,
 )
 from .inputs import GEMMA3_12B, QWEN3_8B, Inputs, make_inputs, rope_tables  # noqa: F401
 
 __all__ = [
     "EPS", "MODELS", "optimized_attention", "attention_prefill", "launch_attention", "prepare_attention",
     "launch_factored_attention", "prepare_factored", "factored_attention", "factored_qk_attention",
-    "norm_rope", "attention_flops", "norm_rope_bytes", "k_prep_bytes", "make_inputs", "rope_tables",
+    "norm_rope", "uses_vt", "transpose_v", "attention_flops", "norm_rope_bytes", "k_prep_bytes", "make_inputs", "rope_tables",
     "Inputs", "QWEN3_8B", "GEMMA3_12B",
 ]

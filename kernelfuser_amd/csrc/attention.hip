@@ -66,6 +66,7 @@ namespace {
 
 struct AttnParams {
   const uint16_t *q, *k, *v, *gq, *cos, *sin;
+  const uint16_t *vt;  // V transposed per head ([B,Hkv,D,S]) for the VT kernels
   uint16_t *out;
   float *inv;
   int64_t S;
@@ -113,9 +114,11 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t bytes)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; it is set right here
 __device__ __forceinline__ void copy16_to_lds(const i32x4_t &rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  // lds and soff are wave-uniform; readfirstlane pins them to SGPRs.
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -283,7 +286,13 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
 //   FOLD = true : GEMM1 starts from -m_run, so s already is logit - m_run
 //                 (Q carries the multiplier); one exp2 per score.  m_run starts
 //                 at 0 and the first tile always sets it to the exact row max.
-template <int D, int BN, bool CAUSAL, bool FOLD = false>
+//   CONSEC = false: P^T operand element j of half g is key
+//                   16*c2 + 8*(j/4) + 4*g + j%4 (the accumulator's own order;
+//                   matches the transpose reads of a row-major V tile);
+//   CONSEC = true : element j of half g is key 16*c2 + 8*g + j (matches
+//                   16-byte reads of V^T rows); two v_permlane32_swap per
+//                   16-key step move the 4-key runs between the half-waves.
+template <int D, int BN, bool CAUSAL, bool FOLD = false, bool CONSEC = false>
 struct Softmax {
   static constexpr int NKB = BN / 32, NK16 = BN / 16, NDB = D / 32;
   float m_run = FOLD ? 0.f : -INFINITY;  // reference max of logits (log2 domain)
@@ -374,12 +383,24 @@ struct Softmax {
     }
     l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
     // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
+    // (registers 4q..4q+3 of a block hold keys 8q + 4*g + 0..3).
 #pragma unroll
     for (int c2 = 0; c2 < NK16; ++c2) {
       u32x4_t wv;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         wv[j] = pack_bf16x2(s[c2 >> 1][8 * (c2 & 1) + 2 * j], s[c2 >> 1][8 * (c2 & 1) + 2 * j + 1]);
+      if constexpr (CONSEC) {
+        // half 0 keeps its keys 0-3 and takes the other half's 4-7; half 1
+        // takes keys 8-11 and keeps its 12-15 (permlane32_swap(a, b) yields
+        // [a_lo, b_lo] and [a_hi, b_hi]).
+        const auto x0 = __builtin_amdgcn_permlane32_swap(wv[0], wv[2], false, false);
+        const auto x1 = __builtin_amdgcn_permlane32_swap(wv[1], wv[3], false, false);
+        wv[0] = x0[0];
+        wv[1] = x1[0];
+        wv[2] = x0[1];
+        wv[3] = x1[1];
+      }
       pb[c2] = as_bf16x8(wv);
     }
   }
@@ -439,13 +460,18 @@ __device__ __forceinline__ void gemm2(const unsigned char *smem, int vbuf, const
 // (the ping-pong kernel's MFMA phase).  Issue order: six reads ahead, one read
 // after each GEMM1 MFMA, two after each GEMM2 MFMA, so every MFMA's operand
 // was requested several MFMAs earlier.
-template <int D, int BN>
+//   VT = false: the V tile is row-major (keys x D); two transpose reads per
+//               GEMM2 MFMA (vra offsets).
+//   VT = true : the tile holds V^T rows (D rows x BN keys, 2*BN bytes each,
+//               chunk ^ ((row >> 1) & 7) swizzle); one 16-byte read per GEMM2
+//               MFMA: row 32*db + lr, chunk 2*c2 + g (vra[c2] + 32*db*2*BN).
+template <int D, int BN, bool VT = false>
 __device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, int vbuf, const uint32_t (&kra)[8],
                                            const uint32_t (&vra)[4], const bf16x8_t (&qreg)[D / 16], float s0,
                                            f32x16_t (&s)[BN / 32], const bf16x8_t (&pb)[BN / 16],
                                            f32x16_t (&o)[D / 32]) {
   constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16, NK16 = BN / 16, NDB = D / 32;
-  constexpr int M1 = NKB * NC, M2 = NK16 * NDB, READS = M1 + 2 * M2, AHEAD = 6;
+  constexpr int M1 = NKB * NC, M2 = NK16 * NDB, READS = M1 + (VT ? 1 : 2) * M2, AHEAD = 6;
 #pragma unroll
   for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -460,10 +486,15 @@ __device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, 
   for (int c2 = 0; c2 < NK16; ++c2) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 3] + (db >> 2) * 256;
-      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
-      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
-      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      bf16x8_t a;
+      if constexpr (VT) {
+        a = *reinterpret_cast<const bf16x8_t *>(smem + vbuf + db * 32 * 2 * BN + vra[c2]);
+      } else {
+        const unsigned char *base = smem + vbuf + 16 * c2 * RB + vra[db & 3] + (db >> 2) * 256;
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 8 * RB));
+        a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
       o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[c2], o[db], 0, 0, 0);
     }
   }
@@ -472,7 +503,7 @@ __device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, 
 #pragma unroll
   for (int i = 0; i < M1 + M2; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    const int want = i < M1 ? 1 : 2;
+    const int want = (i < M1 || VT) ? 1 : 2;
     const int n = issued + want <= READS ? want : READS - issued;
     if (n == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     if (n == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
@@ -502,7 +533,7 @@ __device__ __forceinline__ void store_rows(uint16_t *obase, int qrow, bool qvali
 // ---------------------------------------------------------------------------
 // Ping-pong kernel: D=128, BN=64, two Q heads of a GQA group per workgroup.
 // ---------------------------------------------------------------------------
-template <bool CAUSAL, int PRO, int ST>
+template <bool CAUSAL, int PRO, int ST, bool VT>
 __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   constexpr int D = 128, BN = 64, BM = 128;
   constexpr int TILE = BN * 2 * D;      // 16 KiB
@@ -547,13 +578,21 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 
   const uint32_t head_bytes = (uint32_t)(S * 2 * D);
   const i32x4_t krs = buffer_rsrc(p.k + kvoff * D, head_bytes);
-  const i32x4_t vrs = buffer_rsrc(p.v + kvoff * D, head_bytes);
+  const i32x4_t vrs = buffer_rsrc((VT ? p.vt : p.v) + kvoff * D, head_bytes);
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
   uint32_t kvo[LPW], vvo[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
-    kvo[i] = copy_lane_offset<D>(w * LPW + i, lane, false);
-    vvo[i] = copy_lane_offset<D>(w * LPW + i, lane, true);
+    const int inst = w * LPW + i;
+    kvo[i] = copy_lane_offset<D>(inst, lane, false);
+    if constexpr (VT) {
+      // VT tile: copy inst fills V^T rows 8*inst + lane/8 (2*BN = 128 bytes of
+      // keys each), slot lane%8, swizzle chunk ^ ((row >> 1) & 7).
+      const int row = 8 * inst + lane / 8;
+      vvo[i] = (uint32_t)((lane / 8) * S * 2 + (((lane % 8) ^ ((row >> 1) & 7)) << 4));
+    } else {
+      vvo[i] = copy_lane_offset<D>(inst, lane, true);
+    }
   }
   auto copy_k = [&](int t, int buf) {
 #pragma unroll
@@ -566,7 +605,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int inst = w * LPW + i;
-      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], (uint32_t)(t * TILE + inst * 1024));
+      const uint32_t soff = VT ? (uint32_t)(inst * 8 * S * 2 + t * 2 * BN) : (uint32_t)(t * TILE + inst * 1024);
+      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], soff);
     }
   };
 
@@ -585,11 +625,16 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 
   uint32_t kra[8], vra[4];
   lds_read_offsets<D>(lane, kra, vra);
+  if constexpr (VT) {
+    // V^T reads: row 32*db + lr, chunk 2*c2 + g, swizzled by (row >> 1) & 7.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) vra[j] = (uint32_t)(lr * 2 * BN + (((2 * j + g) ^ ((lr >> 1) & 7)) << 4));
+  }
 
   f32x16_t o[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
-  Softmax<D, BN, CAUSAL, FOLD> sm;
+  Softmax<D, BN, CAUSAL, FOLD, VT> sm;
   f32x16_t s[NKB];
   bf16x8_t pb[NK16];
 #pragma unroll
@@ -626,7 +671,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     constexpr int PAR = decltype(par)::value;
     fence_in(pb);
     fence_in(o);
-    mfma_phase<D, BN>(smem, PAR ? K1 : K0, PAR ? V0 : V1, kra, vra, qreg, sm.acc_init(), s, pb, o);
+    mfma_phase<D, BN, VT>(smem, PAR ? K1 : K0, PAR ? V0 : V1, kra, vra, qreg, sm.acc_init(), s, pb, o);
     fence_regs(s);
     fence_regs(o);
   };
@@ -807,7 +852,10 @@ template <int D, int BN, bool CAUSAL, int PRO, int ST>
 hipError_t launch_t(const AttnParams &p, bool pp, int blocks, hipStream_t s) {
   if constexpr (D == 128) {
     if (pp) {
-      hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST>), dim3(blocks), dim3(512), 0, s, p);
+      if (p.vt)
+        hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST, true>), dim3(blocks), dim3(512), 0, s, p);
+      else
+        hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST, false>), dim3(blocks), dim3(512), 0, s, p);
       return hipGetLastError();
     }
   }
@@ -840,6 +888,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   AttnParams p;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
   p.out = a.out; p.inv = a.inv;
+  p.vt = nullptr;
   p.S = a.S;
   p.B = (int)a.B; p.Hq = (int)a.Hq; p.Hkv = (int)a.Hkv;
   p.eps = a.eps;
@@ -850,6 +899,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   p.n_qblocks = (int)((a.S + BM - 1) / BM);
   const int G = p.Hq / p.Hkv;
   const bool pp = a.D == 128 && G % 2 == 0;
+  if (pp && a.vt && a.S % 8 == 0) p.vt = a.vt;  // V^T rows must be 16-byte aligned
   int blocks;
   if (pp) {
     const int npairs = p.B * p.Hkv * (G / 2);

@@ -122,12 +122,13 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *
   return launch_status(kfmi::launch_rows(a, (hipStream_t)stream), "prepare launch");
 }
 
-static int attention_impl(const void *q, const void *k, const void *v, const void *gq, const void *cos,
-                          const void *sin, void *out, float *inv, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
-                          int64_t D, double scale, float eps, int causal, int prologue, int style, int bm, int bn,
-                          hipStream_t stream) {
+static int attention_impl(const void *q, const void *k, const void *v, const void *vt, const void *gq,
+                          const void *cos, const void *sin, void *out, float *inv, int64_t B, int64_t Hq,
+                          int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal, int prologue,
+                          int style, int bm, int bn, hipStream_t stream) {
   kfmi::AttnArgs a{};
   a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.v = (const uint16_t *)v; a.gq = (const uint16_t *)gq;
+  a.vt = (const uint16_t *)vt;
   a.cos = (const uint16_t *)cos; a.sin = (const uint16_t *)sin; a.out = (uint16_t *)out; a.inv = inv;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
   a.causal = causal != 0; a.prologue = prologue; a.style = style; a.scale = scale; a.eps = eps;
@@ -135,9 +136,10 @@ static int attention_impl(const void *q, const void *k, const void *v, const voi
   return launch_status(kfmi::launch_attention(a, stream), "attention launch");
 }
 
-int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *cos, const void *sin,
-                        void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps,
-                        int causal, int fuse_q, int norm_style, int bm, int bn, void *stream) {
+int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *vt, const void *gq, const void *cos,
+                        const void *sin, void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                        double scale, float eps, int causal, int fuse_q, int norm_style, int bm, int bn,
+                        void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
   KFMI_TRY(check_tiles(bm, bn));
@@ -148,12 +150,13 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_device());
   const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
-  return attention_impl(q, k, v, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
+  if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
+  return attention_impl(q, k, v, vt, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
                         style_of(norm_style), bm, bn, (hipStream_t)stream);
 }
 
 int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
-                               const void *cos, const void *sin, void *out, void *qn, void *kn, int64_t B,
+                               const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt, int64_t B,
                                int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal,
                                int mode, int norm_style, int bm, int bn, void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
@@ -166,9 +169,13 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   if (mode == KFMI_MODE_UNFUSED) KFMI_TRY(check_ptrs({{qn, "qn"}}));
   if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
   if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
+  if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_device());
   const bool rope = cos != nullptr;
+  // V^T is used by the D=128 ping-pong kernel (even GQA ratio) when its rows
+  // are 16-byte aligned.
+  const bool use_vt = vt != nullptr && D == 128 && (Hq / Hkv) % 2 == 0 && S % 8 == 0;
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
   r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;
@@ -176,10 +183,25 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   r.only_k = mode == KFMI_MODE_QUERY; r.rope = rope; r.style = style_of(norm_style); r.eps = eps;
   hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, "prepare launch");
+  if (use_vt) {
+    e = kfmi::launch_transpose_v((const uint16_t *)v, (uint16_t *)vt, B * Hkv, S, D, (hipStream_t)stream);
+    if (e != hipSuccess) return launch_status(e, "V transpose launch");
+  }
   const bool query = mode == KFMI_MODE_QUERY;
   const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
-  return attention_impl(query ? q : qn, kn, v, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
-                        style_of(norm_style), bm, bn, (hipStream_t)stream);
+  return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D,
+                        scale, eps, causal, pro, style_of(norm_style), bm, bn, (hipStream_t)stream);
+}
+
+int kfmi_transpose_v_bf16(const void *v, void *vt, int64_t BH, int64_t S, int64_t D, void *stream) {
+  if (BH < 1 || S < 1) return fail(KFMI_EINVAL, "BH and S must be >= 1");
+  if (D != 128 && D != 256) return fail(KFMI_EINVAL, "D must be 128 or 256 (got %lld)", (long long)D);
+  if (S % 8 != 0) return fail(KFMI_EINVAL, "S must be a multiple of 8 (got %lld)", (long long)S);
+  if (BH * S * D >= ((int64_t)1 << 31)) return fail(KFMI_EINVAL, "tensors must have fewer than 2^31 elements");
+  KFMI_TRY(check_ptrs({{v, "v"}, {vt, "vt"}}));
+  KFMI_TRY(check_device());
+  return launch_status(kfmi::launch_transpose_v((const uint16_t *)v, (uint16_t *)vt, BH, S, D, (hipStream_t)stream),
+                       "V transpose launch");
 }
 
 int kfmi_factored_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk, float *inv, void *kn,
@@ -207,7 +229,7 @@ int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, f
   if (inv && (reinterpret_cast<uintptr_t>(inv) & 3u)) return fail(KFMI_EINVAL, "inv must be 4-byte aligned");
   KFMI_TRY(check_device());
   const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
-  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
                         kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
 }
 
@@ -226,7 +248,7 @@ int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void
   r.only_k = true; r.rope = false; r.style = kfmi::ST_FACTORED; r.eps = eps;
   hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, "factored prepare launch");
-  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
                         kfmi::PRO_FACTORED_CALC, kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
 }
 

@@ -35,6 +35,7 @@ struct RowsArgs {
 
 struct AttnArgs {
   const uint16_t *q, *k, *v, *gq, *cos, *sin;
+  const uint16_t *vt;  // V transposed per head ([B,Hkv,D,S]) or NULL
   uint16_t *out;
   float *inv;
   int64_t B, Hq, Hkv, S, D;
@@ -47,6 +48,8 @@ struct AttnArgs {
 
 // Both return hipSuccess or the launch error.  Arguments are validated by the caller.
 hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
+// vt[b,h,d,s] = v[b,h,s,d] for the B*H heads of S rows of D.
+hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64_t S, int64_t D, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
 
 }  // namespace kfmi

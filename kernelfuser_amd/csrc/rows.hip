@@ -183,7 +183,69 @@ hipError_t dispatch_rows(const RowsParams &p, int style, bool rope, int bx, int 
   return hipErrorInvalidValue;
 }
 
+// V -> VT per head: one workgroup moves a tile of 64 rows x D columns.  The
+// rows are read with coalesced 16-byte loads into a row-major LDS tile whose
+// 16-byte chunks are XOR-swizzled (chunk ^ 4*(row % 4)), then read back with
+// ds_read_b64_tr_b16: two transpose reads give a lane 8 consecutive rows of
+// one column, i.e. 16 contiguous bytes of a VT row, stored with one 16-byte
+// write.  Rows past S load as zeros and are not stored.  Requires S % 8 == 0
+// (16-byte aligned VT rows); the host checks it.
+template <int D>
+__global__ __launch_bounds__(256) void transpose_v_kernel(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt,
+                                                          int64_t S) {
+  constexpr int TR = 64;      // rows per tile
+  constexpr int RB = 2 * D;   // bytes per row
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  __shared__ __attribute__((aligned(16))) unsigned char tile[TR * RB];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5;
+  const int64_t bh = blockIdx.y;
+  const int64_t s0 = (int64_t)blockIdx.x * TR;
+  const uint16_t *src = v + (bh * S + s0) * D;
+  const int rows = (int)((S - s0) < TR ? (S - s0) : TR);
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < TR * CPR / 256; ++i) {
+    const int e = tid + 256 * i;
+    const int r = e / CPR, c = e % CPR;
+    const u32x4_t x = r < rows ? ld16(src + (int64_t)r * D + 8 * c) : zero;
+    *reinterpret_cast<u32x4_t *>(tile + r * RB + ((c ^ ((r & 3) << 2)) << 4)) = x;
+  }
+  __syncthreads();
+  // Transpose reads: the 16-lane group supplies rows (lane%16)/4 + 8g (and +4
+  // for the second read) of a 16-row step and 4-column runs
+  // 16*((lane/16)%2) + 4*(lane%4) of a 32-wide column block; lane l then holds
+  // rows 16*c2 + 8g .. +7, in order, of column 32*db + l%32.
+  const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
+  const int row0 = ((lane & 15) >> 2) + 8 * g;
+  constexpr int NBLK = (TR / 16) * (D / 32);
+  uint16_t *dst = vt + bh * D * S;
+#pragma unroll
+  for (int i = 0; i < NBLK / 4; ++i) {
+    const int blk = w * (NBLK / 4) + i;
+    const int c2 = blk / (D / 32), db = blk % (D / 32);
+    const int chunk0 = 4 * db + 2 * hh + kk;  // chunk of the lane's 8-byte run
+    const unsigned char *base = tile + (16 * c2 + row0) * RB + ((chunk0 ^ (m << 2)) << 4) + (lane & 1) * 8;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 4 * RB));
+    const int r = 16 * c2 + 8 * g;
+    if (r < rows) {
+      const u32x4_t x = __builtin_bit_cast(u32x4_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      st16(dst + (int64_t)(32 * db + (lane & 31)) * S + s0 + r, x);
+    }
+  }
+}
+
 }  // namespace
+
+hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64_t S, int64_t D, hipStream_t stream) {
+  const dim3 grid((unsigned)((S + 63) / 64), (unsigned)BH);
+  if (D == 128) {
+    hipLaunchKernelGGL((transpose_v_kernel<128>), grid, dim3(256), 0, stream, v, vt, S);
+  } else {
+    hipLaunchKernelGGL((transpose_v_kernel<256>), grid, dim3(256), 0, stream, v, vt, S);
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   RowsParams p;

@@ -75,13 +75,18 @@ def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_nor
 
 
 def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, warps=4, stages=1,
-                     gather=True, rope=True, hf_norm=True, qn=None, kn=None, norm_style=None):
+                     gather=True, rope=True, hf_norm=True, qn=None, kn=None, norm_style=None, vt=None):
     """Preparation + attention launches of the reference launcher (rope:661-677).
 
     ``mode='query'``: K is prepared once into ``kn``; Q's norm (+RoPE) runs in the
     attention prologue.  ``mode='unfused'``: Q into ``qn`` and K into ``kn``, then
     plain attention.  Scratch buffers must be preallocated (rope:665-672).  Timings
-    must include both launches, as this function issues them.
+    must include every launch, as this function issues them.
+
+    ``vt`` (optional, shaped like V): scratch for V transposed per head.  When
+    given (and D=128, an even GQA ratio and S % 8 == 0), the preparation launch
+    also writes it and the attention kernel reads V^T rows, which halves its
+    LDS reads of V; results are identical.
     """
     if mode not in ("full", "query", "unfused"):
         raise ValueError("Invalid fusion mode")
@@ -96,22 +101,31 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
     _lib.call("kfmi_launch_attention_bf16",
               ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk),
               ptr(cos) if rope else None, ptr(sin) if rope else None,
-              ptr(out), ptr(qn), ptr(kn),
+              ptr(out), ptr(qn), ptr(kn), ptr(vt),
               b, h, k.shape[1], s, d, float(d) ** -0.5, EPS, int(bool(causal)),
               MODE_QUERY if mode == "query" else MODE_UNFUSED, _style(norm_style, hf_norm),
               _bm(bm), _bn(bn), stream_of(q))
 
 
 def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=False, fuse_q=True,
-                      norm_style="fp32", bm=128, bn=64, scale=None):
+                      norm_style="fp32", bm=128, bn=64, scale=None, vt=None):
     """The attention launch alone (attention_v2_kernel, rope:608-649) on a prepared
     ``kn``.  ``fuse_q=True``: raw ``q`` with its RMSNorm (``gq``) and, when both
     tables are given, RoPE in the prologue (FUSE_Q); ``fuse_q=False``: ``q`` is
-    already prepared.  ``scale`` defaults to D^-1/2 (rope:676)."""
+    already prepared.  ``scale`` defaults to D^-1/2 (rope:676).  ``vt``: V
+    transposed per head (see ``transpose_v``), read instead of ``v`` when the
+    shape allows it (``uses_vt``)."""
     b, h, s, d = q.shape
-    _lib.call("kfmi_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(gq), ptr(cos), ptr(sin), ptr(out),
+    _lib.call("kfmi_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(vt), ptr(gq), ptr(cos), ptr(sin), ptr(out),
               b, h, kn.shape[1], s, d, float(d) ** -0.5 if scale is None else float(scale), EPS,
               int(bool(causal)), int(bool(fuse_q)), NORM_STYLES[norm_style], _bm(bm), _bn(bn), stream_of(q))
+
+
+def transpose_v(v, vt):
+    """``vt[b,h,d,s] = v[b,h,s,d]`` (S % 8 == 0): the V^T scratch that
+    ``launch_attention`` fills itself when given ``vt``."""
+    b, h, s, d = v.shape
+    _lib.call("kfmi_transpose_v_bf16", ptr(v), ptr(vt), b * h, s, d, stream_of(v))
 
 
 def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=64):
@@ -261,12 +275,18 @@ def _optimized_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g
     out = torch.empty_like(q)
     kn = torch.empty_like(k)
     qn = torch.empty_like(q) if mode == "unfused" else None
+    vt = torch.empty_like(v) if uses_vt(q.shape[1], k.shape[1], q.shape[2], q.shape[3]) else None
     rotary = cos is not None
     xs = (q, k, v, gq, gk, cos if rotary else q, sin if rotary else k)
     with torch.cuda.device(q.device):
         launch_attention(xs, out, causal=causal, mode=mode, bm=128, bn=bn, rope=rotary, qn=qn, kn=kn,
-                         norm_style=norm_style)
+                         norm_style=norm_style, vt=vt)
     return out
+
+
+def uses_vt(hq: int, hkv: int, s: int, d: int) -> bool:
+    """Whether launch_attention makes use of a ``vt`` scratch for this shape."""
+    return d == 128 and (hq // hkv) % 2 == 0 and s % 8 == 0
 
 
 @_optimized_attention_op.register_fake

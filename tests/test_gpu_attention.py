@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle
-from helpers import announce
+from helpers import announce, bf16_ulp
 from kernelfuser_amd import QWEN3_8B, launch_attention, make_inputs, optimized_attention
 
 pytestmark = pytest.mark.gpu
@@ -132,3 +132,43 @@ def test_launch_attention_buffers(gpu):
         launch_attention(xs.reference7, out, mode="unfused", kn=kn)
     with pytest.raises(ValueError):
         launch_attention(xs.reference7, out, mode="bad", kn=kn)
+
+
+@pytest.mark.parametrize("b,s,causal", [(1, 1000, True), (2, 256, False), (1, 64, True), (1, 129, True)])
+def test_vt_path_identical(gpu, b, s, causal):
+    """The V^T scratch path (preparation writes V transposed per head, the
+    kernel reads V^T rows) agrees with the row-major V path (the MFMA sums the
+    same products of each 16-key step, possibly in another order, so results
+    may differ in the last bit of a few outputs); shapes it does not apply to
+    (S % 8 != 0) leave the scratch untouched."""
+    from kernelfuser_amd import uses_vt
+    xs = make_inputs(b, s, QWEN3_8B, 606).to(gpu)
+    out1, kn1 = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    out2, kn2 = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    vt = torch.full_like(xs.v, 3.0)
+    announce(f"attention vt path B={b} S={s} causal={causal}")
+    launch_attention(xs.reference7, out1, causal=causal, mode="query", kn=kn1, norm_style="fp32")
+    launch_attention(xs.reference7, out2, causal=causal, mode="query", kn=kn2, norm_style="fp32", vt=vt)
+    torch.cuda.synchronize()
+    # one BF16 ulp, plus FP32 summation-order noise for outputs that cancel to ~0
+    diff = (out1.float() - out2.float()).abs()
+    tol = bf16_ulp(torch.maximum(out1.float().abs(), out2.float().abs())) * 1.01 + 1e-5
+    assert bool((diff <= tol).all()), float((diff / tol).max())
+    assert float((diff > 0).float().mean()) < 0.02
+    assert torch.equal(kn1, kn2)
+    if uses_vt(32, 8, s, 128):
+        assert torch.equal(vt, xs.v.transpose(2, 3).contiguous().view_as(vt))
+    else:
+        assert bool((vt == 3.0).all())
+    ref = oracle.oracle_fp32(*[t.cpu() for t in xs.astuple()], causal)
+    assert oracle.attention_gate(out2.cpu(), ref)["pass"]
+
+
+def test_transpose_v_d256(gpu):
+    from kernelfuser_amd import transpose_v
+    v = (torch.randn(2, 3, 200, 256, generator=torch.Generator().manual_seed(3))).to(torch.bfloat16).to(gpu)
+    vt = torch.empty_like(v)
+    announce("transpose_v D=256 S=200")
+    transpose_v(v, vt)
+    torch.cuda.synchronize()
+    assert torch.equal(vt.view(2, 3, 256, 200), v.transpose(2, 3))
