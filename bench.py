@@ -68,20 +68,37 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_launches(fn, n, warmup=3):
-    """Average device time (ms) of ``fn`` over ``n`` back-to-back calls, measured
-    with HIP events on torch's current stream (the stream the kernels use)."""
+def time_graph(fn, n, replays=10):
+    """Average device time (ms) per call of ``fn(i)``, i = 0..n-1, captured
+    into one HIP graph (torch.cuda.CUDAGraph) and replayed ``replays`` times
+    after warmup replays: the launch-rate-independent timing of the
+    reference's harness (src/fusion_harness.py:32-79).  Median over replays."""
     import torch
-    for _ in range(warmup):
-        fn(0)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for i in range(min(n, 3)):
+            fn(i)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n):
+                fn(i)
+    torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
-    a, b = _events()
-    a.record()
-    for i in range(n):
-        fn(i)
-    b.record()
-    b.synchronize()
-    return a.elapsed_time(b) / n
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        a, b = _events()
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) / n)
+    del graph
+    return statistics.median(times)
 
 
 def load_traffic():
@@ -122,16 +139,19 @@ def headline(args, torch, kf):
     res = {"flops_per_step": flops, "ms_per_step": ms_step, "device_ms_per_step": dev_ms / args.steps,
            "tflops": flops / (ms_step * 1e-3) / 1e12}
     # The two kernels separately (events on the launch stream).
-    attn_ms = time_launches(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
+    attn_ms = time_graph(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
                                                            causal=True, fuse_q=True, norm_style=args.norm_style,
                                                            vt=vt),
-                            max(args.steps, 20))
-    prep_ms = time_launches(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
-                                                           norm_style=args.norm_style), max(args.steps, 20))
+                         20)
+    # The preparation launch of the step: K norm+RoPE rows plus V^T.
+    prep_ms = time_graph(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
+                                                        norm_style=args.norm_style, vt=vt), 100)
     res["attention_kernel_us"] = attn_ms * 1e3
-    res["k_prep_kernel_us"] = prep_ms * 1e3
+    res["prep_kernel_us"] = prep_ms * 1e3
     res["attention_kernel_tflops"] = flops / (attn_ms * 1e-3) / 1e12
-    res["k_prep_gbs"] = kf.k_prep_bytes(b, hkv, s, d) / (prep_ms * 1e-3) / 1e9
+    prep_bytes = kf.k_prep_bytes(b, hkv, s, d) + 2 * xs.v.numel() * 2
+    res["prep_bytes"] = prep_bytes
+    res["prep_gbs"] = prep_bytes / (prep_ms * 1e-3) / 1e9
     return res, xs_cpu, out
 
 
@@ -150,8 +170,7 @@ def norm_rope_sweep(args, torch, kf):
             sets.append((q, k, torch.empty_like(q), torch.empty_like(k)))
         fn = lambda i: kf.norm_rope(sets[i % nsets][0], sets[i % nsets][1], base.gq, base.gk, base.cos, base.sin,
                                     norm_style=args.norm_style, qn=sets[i % nsets][2], kn=sets[i % nsets][3])
-        n = max(4 * nsets, 40)
-        ms = time_launches(fn, n, warmup=nsets)
+        ms = time_graph(fn, max(4 * nsets, 40))
         rows.append({"B": b, "S": s, "bytes": nbytes, "us": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
                      "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "buffer_sets": nsets})
         del sets, base
@@ -170,13 +189,13 @@ def prefill_shapes(args, torch, kf):
     rows = []
     for b, s in [(1, 2048), (1, 8192), (4, 1000)]:
         xs = kf.make_inputs(b, s, QWEN3_8B, 2909).to("cuda:0")
-        out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
-        ms = time_launches(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
-                                                          bn=64, kn=kn, norm_style=args.norm_style), 20)
+        out, kn, vt = torch.empty_like(xs.q), torch.empty_like(xs.k), torch.empty_like(xs.v)
+        ms = time_graph(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
+                                                       bn=64, kn=kn, norm_style=args.norm_style, vt=vt), 20)
         f = kf.attention_flops(b, hq, s, d, True)
         rows.append({"B": b, "S": s, "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
                      "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS})
-        del xs, out, kn
+        del xs, out, kn, vt
     return rows
 
 
@@ -186,8 +205,8 @@ def factored(args, torch, kf):
     xs = kf.make_inputs(b, s, GEMMA3_12B, 1909, rope=False).to("cuda:0")
     out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
     inv = torch.empty(xs.q.shape[:-1], device="cuda:0", dtype=torch.float32)
-    ms = time_launches(lambda i: kf.launch_factored_attention((xs.q, xs.k, xs.v, xs.gq, xs.gk), out, inv, kn,
-                                                              causal=True, bm=128, bn=64), 20)
+    ms = time_graph(lambda i: kf.launch_factored_attention((xs.q, xs.k, xs.v, xs.gq, xs.gk), out, inv, kn,
+                                                           causal=True, bm=128, bn=64), 20)
     f = kf.attention_flops(b, hq, s, d, True)
     return {"B": b, "S": s, "Hq": hq, "Hkv": hkv, "D": d, "causal": True, "us": ms * 1e3,
             "tflops": f / (ms * 1e-3) / 1e12, "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS}
@@ -249,9 +268,10 @@ def pmc_run(torch, kf):
     """A few launches of each kernel at the headline shapes plus one copy of
     known size, for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE)."""
     xs = kf.make_inputs(1, 4096, QWEN3_8B, 1909).to("cuda:0")
-    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    out, kn, vt = torch.empty_like(xs.q), torch.empty_like(xs.k), torch.empty_like(xs.v)
     for _ in range(3):
-        kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn, norm_style="fp32")
+        kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn, norm_style="fp32",
+                            vt=vt)
     nr = kf.make_inputs(1, 8192, QWEN3_8B, 1909, with_v=False).to("cuda:0")
     qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
     for _ in range(3):
@@ -303,12 +323,14 @@ def main():
                    "B": args.batch, "S": args.seq, "Hq": 32, "Hkv": 8, "D": 128, "causal": True,
                    "norm_style": args.norm_style, "flops_per_step": head["flops_per_step"],
                    "flops_convention": "4*B*Hq*D*S(S+1)/2"},
-        "roofline": {"bound": "mfma", "kernel": "attn_fwd_kernel (fused Q norm+RoPE prologue)",
+        "roofline": {"bound": "mfma", "kernel": "attn_pp_kernel (fused Q norm+RoPE prologue, ping-pong waves)",
                      "achieved": head["attention_kernel_tflops"], "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                      "frac": head["attention_kernel_tflops"] / MFMA_BF16_PEAK_TFS,
                      "kernel_us": head["attention_kernel_us"], "traffic": traffic},
-        "kernels": {"attention_us": head["attention_kernel_us"], "k_prep_us": head["k_prep_kernel_us"],
-                    "k_prep_gbs": head["k_prep_gbs"], "device_ms_per_step": head["device_ms_per_step"]},
+        "kernels": {"attention_us": head["attention_kernel_us"],
+                    "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
+                    "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows and V^T in one launch",
+                    "device_ms_per_step": head["device_ms_per_step"]},
     }
     if not args.quick:
         line["norm_rope"] = norm_rope_sweep(args, torch, kf)

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 2
+#define KFMI_ABI_VERSION 3
 
 /* status codes */
 #define KFMI_OK 0
@@ -64,9 +64,13 @@ const char *kfmi_last_error(void);
  * (rope:652-658, :585-605, row math :550-582).  Q rows are skipped when
  * flags has KFMI_PREP_ONLY_K (q and qn may then be NULL); cos/sin are read
  * only when flags has KFMI_PREP_ROPE.  Also serves the isolated Q/K norm+RoPE
- * workload (Q and K rows in one launch). */
-int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk,
-                      const void *cos, const void *sin, void *qn, void *kn,
+ * workload (Q and K rows in one launch).
+ * vt (may be NULL; then v is ignored): the same launch also writes V
+ * transposed per head, vt[b,h,d,s] = v[b,h,s,d] (D == 128, S % 8 == 0) -- the
+ * V^T operand of kfmi_attention_bf16.  This addition has no counterpart in
+ * the reference, whose kernels read V directly. */
+int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                      const void *cos, const void *sin, void *qn, void *kn, void *vt,
                       int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                       float eps, int norm_style, int flags, void *stream);
 
@@ -79,8 +83,8 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *
  * rope:676).  bm is the number of query rows per workgroup (multiple of 32;
  * 128 is the tuned value), bn the key tile (64 or 128; a scheduling hint,
  * results do not depend on it).  vt (optional, may be NULL): V transposed per
- * head ([B,Hkv,D,S], as written by kfmi_transpose_v_bf16); used instead of v
- * under the conditions given at kfmi_launch_attention_bf16. */
+ * head ([B,Hkv,D,S], as written by kfmi_prepare_bf16 or kfmi_transpose_v_bf16);
+ * used instead of v under the conditions given at kfmi_launch_attention_bf16. */
 int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *vt, const void *gq,
                         const void *cos, const void *sin, void *out,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
@@ -95,8 +99,9 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
  * vt (optional, may be NULL): caller-allocated scratch of V's size; when
  * given and D == 128, Hq/Hkv is even and S % 8 == 0, the preparation launch
  * also writes V transposed per head ([B,Hkv,D,S]) and the attention kernel
- * reads that instead of V (one LDS read per V operand instead of two).
- * Results are identical either way. */
+ * reads that instead of V (one 16-byte LDS read per V operand instead of two
+ * transposing 8-byte reads).  Results are identical either way; the call
+ * stays two launches. */
 int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
                                const void *gq, const void *gk, const void *cos,
                                const void *sin, void *out, void *qn, void *kn, void *vt,

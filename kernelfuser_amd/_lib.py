@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -29,7 +29,7 @@ _D = ctypes.c_double
 
 # name -> argtypes (restype is int for all compute entry points)
 SIGNATURES = {
-    "kfmi_prepare_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
+    "kfmi_prepare_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
     "kfmi_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D, _F, _I, _I, _I, _I, _I,
                             _P],
     "kfmi_transpose_v_bf16": [_P, _P, _I64, _I64, _I64, _P],

@@ -101,8 +101,8 @@ int kfmi_abi_version(void) { return KFMI_ABI_VERSION; }
 
 const char *kfmi_last_error(void) { return g_error.c_str(); }
 
-int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *gk, const void *cos,
-                      const void *sin, void *qn, void *kn, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
+int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk, const void *cos,
+                      const void *sin, void *qn, void *kn, void *vt, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
                       int64_t D, float eps, int norm_style, int flags, void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
@@ -112,8 +112,13 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *gq, const void *
   if (!only_k) KFMI_TRY(check_ptrs({{q, "q"}, {gq, "gq"}, {qn, "qn"}}));
   if (rope) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
+  if (vt) {
+    KFMI_TRY(check_ptrs({{v, "v"}, {vt, "vt"}}));
+    if (D != 128 || S % 8 != 0) return fail(KFMI_EINVAL, "vt needs D == 128 and S % 8 == 0");
+  }
   KFMI_TRY(check_device());
   kfmi::RowsArgs a{};
+  a.v = (const uint16_t *)v; a.vt = (uint16_t *)vt;
   a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.gq = (const uint16_t *)gq; a.gk = (const uint16_t *)gk;
   a.cos = (const uint16_t *)cos; a.sin = (const uint16_t *)sin;
   a.qn = (uint16_t *)qn; a.kn = (uint16_t *)kn; a.inv = nullptr;
@@ -181,12 +186,12 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;
   r.B = B; r.Hq = Hq; r.Hkv = Hkv; r.S = S; r.D = D;
   r.only_k = mode == KFMI_MODE_QUERY; r.rope = rope; r.style = style_of(norm_style); r.eps = eps;
+  if (use_vt) {  // the preparation launch also writes V^T
+    r.v = (const uint16_t *)v;
+    r.vt = (uint16_t *)vt;
+  }
   hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, "prepare launch");
-  if (use_vt) {
-    e = kfmi::launch_transpose_v((const uint16_t *)v, (uint16_t *)vt, B * Hkv, S, D, (hipStream_t)stream);
-    if (e != hipSuccess) return launch_status(e, "V transpose launch");
-  }
   const bool query = mode == KFMI_MODE_QUERY;
   const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D,

@@ -27,6 +27,8 @@ struct RowsArgs {
   const uint16_t *q, *k, *gq, *gk, *cos, *sin;
   uint16_t *qn, *kn;
   float *inv;
+  const uint16_t *v;  // with vt: V to transpose per head in the same launch (D = 128, S % 8 == 0)
+  uint16_t *vt;       // NULL: no transpose
   int64_t B, Hq, Hkv, S, D;
   bool only_k, rope;
   int style;

@@ -23,11 +23,67 @@ struct RowsParams {
   const uint16_t *q, *k, *gq, *gk, *cos, *sin;
   uint16_t *qn, *kn;
   float *inv;
+  const uint16_t *v;  // V, transposed into vt by the extra workgroups (VT kernels)
+  uint16_t *vt;
   int64_t S;
   int B, Hq_rows, Hq, Hkv;  // Hq_rows = Q heads processed (0 = K rows only); Hq = Q tensor heads
   int heads_per_chunk, n_groups;
+  int rows_by;              // grid rows (blockIdx.y) of the row work; VT tiles follow
+  int vt_sblocks;           // 64-row tiles per head of V
+  int64_t vt_tiles;         // B * Hkv * vt_sblocks
   float eps;
 };
+
+// V -> VT per head, one 64-row tile (rows s0..s0+63 of head bh) per
+// workgroup of 256 threads.  The rows are read with coalesced 16-byte loads
+// into a row-major LDS tile whose 16-byte chunks are XOR-swizzled
+// (chunk ^ 4*(row % 4)), then read back with ds_read_b64_tr_b16: two
+// transpose reads give a lane 8 consecutive rows of one column, i.e. 16
+// contiguous bytes of a VT row, stored with one 16-byte write.  Rows past S
+// load as zeros and are not stored.  Requires S % 8 == 0 (16-byte aligned VT
+// rows); the host checks it.
+template <int D>
+__device__ __forceinline__ void transpose_tile(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt, int64_t S,
+                                               int64_t bh, int64_t s0) {
+  constexpr int TR = 64;      // rows per tile
+  constexpr int RB = 2 * D;   // bytes per row
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  __shared__ __attribute__((aligned(16))) unsigned char tile[TR * RB];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5;
+  const uint16_t *src = v + (bh * S + s0) * D;
+  const int rows = (int)((S - s0) < TR ? (S - s0) : TR);
+  const u32x4_t zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < TR * CPR / 256; ++i) {
+    const int e = tid + 256 * i;
+    const int r = e / CPR, c = e % CPR;
+    const u32x4_t x = r < rows ? ld16_nt(src + (int64_t)r * D + 8 * c) : zero;
+    *reinterpret_cast<u32x4_t *>(tile + r * RB + ((c ^ ((r & 3) << 2)) << 4)) = x;
+  }
+  __syncthreads();
+  // Transpose reads: the 16-lane group supplies rows (lane%16)/4 + 8g (and +4
+  // for the second read) of a 16-row step and 4-column runs
+  // 16*((lane/16)%2) + 4*(lane%4) of a 32-wide column block; lane l then holds
+  // rows 16*c2 + 8g .. +7, in order, of column 32*db + l%32.
+  const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
+  const int row0 = ((lane & 15) >> 2) + 8 * g;
+  constexpr int NBLK = (TR / 16) * (D / 32);
+  uint16_t *dst = vt + bh * D * S;
+#pragma unroll
+  for (int i = 0; i < NBLK / 4; ++i) {
+    const int blk = w * (NBLK / 4) + i;
+    const int c2 = blk / (D / 32), db = blk % (D / 32);
+    const int chunk0 = 4 * db + 2 * hh + kk;  // chunk of the lane's 8-byte run
+    const unsigned char *base = tile + (16 * c2 + row0) * RB + ((chunk0 ^ (m << 2)) << 4) + (lane & 1) * 8;
+    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
+    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 4 * RB));
+    const int r = 16 * c2 + 8 * g;
+    if (r < rows) {
+      const u32x4_t x = __builtin_bit_cast(u32x4_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      st16(dst + (int64_t)(32 * db + (lane & 31)) * S + s0 + r, x);
+    }
+  }
+}
 
 // Normalised element x*inv*gamma with the rounding points of a style.
 template <int ST>
@@ -69,12 +125,34 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
-template <int D, int ST, bool ROPE, bool ONLY_K>
+#ifndef KFMI_ROWS_U
+#define KFMI_ROWS_U 2
+#endif
+#ifndef KFMI_ROWS_WAVES
+#define KFMI_ROWS_WAVES 16384
+#endif
+#ifndef KFMI_ROWS_NT
+#define KFMI_ROWS_NT 1
+#endif
+__device__ __forceinline__ u32x4_t ld_row(const uint16_t *p) { return KFMI_ROWS_NT ? ld16_nt(p) : ld16(p); }
+__device__ __forceinline__ void st_row(uint16_t *p, const u32x4_t &v) {
+  if (KFMI_ROWS_NT) st16_nt(p, v); else st16(p, v);
+}
+
+template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
 __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPW = 64 / LPR;  // positions per wave
   constexpr int HALF = LPR / 2;
-  constexpr int U = 4;           // heads in flight per lane
+  constexpr int U = KFMI_ROWS_U;  // heads in flight per lane
+  if constexpr (VT) {
+    // Grid rows past the row work transpose V tiles (same launch).
+    if ((int)blockIdx.y >= p.rows_by) {
+      const int64_t t = (int64_t)(blockIdx.y - p.rows_by) * gridDim.x + blockIdx.x;
+      if (t < p.vt_tiles) transpose_tile<D>(p.v, p.vt, p.S, t / p.vt_sblocks, (t % p.vt_sblocks) * 64);
+      return;  // workgroup-uniform
+    }
+  }
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wave >= p.B * p.n_groups) return;  // wave-uniform
@@ -110,7 +188,7 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
       const uint16_t *src = hh < Hq_rows
                                 ? p.q + (((int64_t)b * p.Hq + hh) * p.S + pos) * D + d0
                                 : p.k + (((int64_t)b * p.Hkv + (hh - Hq_rows)) * p.S + pos) * D + d0;
-      xv[u] = (hh < h_end && valid) ? ld16(src) : zero;
+      xv[u] = (hh < h_end && valid) ? ld_row(src) : zero;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -135,7 +213,7 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
           unpack8(gq_fac, gq);
 #pragma unroll
           for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), gk[j]), gq[j]);
-          if (valid) st16(p.kn + row * D + d0, pack8(y));
+          if (valid) st_row(p.kn + row * D + d0, pack8(y));
         }
       } else {
         float go[8], y[8];
@@ -155,21 +233,29 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
           for (int j = 0; j < 8; ++j) y[j] = norm_elem<ST>(x[j], inv, go[j]);
         }
         uint16_t *dst = (is_q ? p.qn : p.kn) + row * D + d0;
-        if (valid) st16(dst, pack8(y));
+        if (valid) st_row(dst, pack8(y));
       }
     }
   }
 }
 
-template <int D, int ST, bool ROPE, bool ONLY_K>
+template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
 hipError_t launch_rows_t(const RowsParams &p, int blocks_x, int blocks_y, hipStream_t stream) {
-  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K>), dim3(blocks_x, blocks_y), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT>), dim3(blocks_x, blocks_y), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int D, int ST, bool ROPE>
 hipError_t dispatch_k(const RowsParams &p, int bx, int by, hipStream_t s) {
-  return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false>(p, bx, by, s) : launch_rows_t<D, ST, ROPE, true>(p, bx, by, s);
+  if constexpr (D == 128 && ST != ST_FACTORED) {
+    if (p.vt) {
+      const int by_all = by + (int)((p.vt_tiles + bx - 1) / bx);
+      return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false, true>(p, bx, by_all, s)
+                       : launch_rows_t<D, ST, ROPE, true, true>(p, bx, by_all, s);
+    }
+  }
+  return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false, false>(p, bx, by, s)
+                   : launch_rows_t<D, ST, ROPE, true, false>(p, bx, by, s);
 }
 
 template <int D>
@@ -183,56 +269,10 @@ hipError_t dispatch_rows(const RowsParams &p, int style, bool rope, int bx, int 
   return hipErrorInvalidValue;
 }
 
-// V -> VT per head: one workgroup moves a tile of 64 rows x D columns.  The
-// rows are read with coalesced 16-byte loads into a row-major LDS tile whose
-// 16-byte chunks are XOR-swizzled (chunk ^ 4*(row % 4)), then read back with
-// ds_read_b64_tr_b16: two transpose reads give a lane 8 consecutive rows of
-// one column, i.e. 16 contiguous bytes of a VT row, stored with one 16-byte
-// write.  Rows past S load as zeros and are not stored.  Requires S % 8 == 0
-// (16-byte aligned VT rows); the host checks it.
 template <int D>
 __global__ __launch_bounds__(256) void transpose_v_kernel(const uint16_t *__restrict__ v, uint16_t *__restrict__ vt,
                                                           int64_t S) {
-  constexpr int TR = 64;      // rows per tile
-  constexpr int RB = 2 * D;   // bytes per row
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  __shared__ __attribute__((aligned(16))) unsigned char tile[TR * RB];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 5;
-  const int64_t bh = blockIdx.y;
-  const int64_t s0 = (int64_t)blockIdx.x * TR;
-  const uint16_t *src = v + (bh * S + s0) * D;
-  const int rows = (int)((S - s0) < TR ? (S - s0) : TR);
-  const u32x4_t zero = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int i = 0; i < TR * CPR / 256; ++i) {
-    const int e = tid + 256 * i;
-    const int r = e / CPR, c = e % CPR;
-    const u32x4_t x = r < rows ? ld16(src + (int64_t)r * D + 8 * c) : zero;
-    *reinterpret_cast<u32x4_t *>(tile + r * RB + ((c ^ ((r & 3) << 2)) << 4)) = x;
-  }
-  __syncthreads();
-  // Transpose reads: the 16-lane group supplies rows (lane%16)/4 + 8g (and +4
-  // for the second read) of a 16-row step and 4-column runs
-  // 16*((lane/16)%2) + 4*(lane%4) of a 32-wide column block; lane l then holds
-  // rows 16*c2 + 8g .. +7, in order, of column 32*db + l%32.
-  const int m = (lane >> 2) & 3, hh = (lane >> 4) & 1, kk = (lane >> 1) & 1;
-  const int row0 = ((lane & 15) >> 2) + 8 * g;
-  constexpr int NBLK = (TR / 16) * (D / 32);
-  uint16_t *dst = vt + bh * D * S;
-#pragma unroll
-  for (int i = 0; i < NBLK / 4; ++i) {
-    const int blk = w * (NBLK / 4) + i;
-    const int c2 = blk / (D / 32), db = blk % (D / 32);
-    const int chunk0 = 4 * db + 2 * hh + kk;  // chunk of the lane's 8-byte run
-    const unsigned char *base = tile + (16 * c2 + row0) * RB + ((chunk0 ^ (m << 2)) << 4) + (lane & 1) * 8;
-    const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base));
-    const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t *)(base + 4 * RB));
-    const int r = 16 * c2 + 8 * g;
-    if (r < rows) {
-      const u32x4_t x = __builtin_bit_cast(u32x4_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-      st16(dst + (int64_t)(32 * db + (lane & 31)) * S + s0 + r, x);
-    }
-  }
+  transpose_tile<D>(v, vt, S, blockIdx.y, (int64_t)blockIdx.x * 64);
 }
 
 }  // namespace
@@ -251,6 +291,7 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   RowsParams p;
   p.q = a.q; p.k = a.k; p.gq = a.gq; p.gk = a.gk; p.cos = a.cos; p.sin = a.sin;
   p.qn = a.qn; p.kn = a.kn; p.inv = a.inv;
+  p.v = a.v; p.vt = a.vt;
   p.S = a.S;
   p.B = (int)a.B;
   p.Hq = (int)a.Hq;
@@ -264,11 +305,15 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   // Split the heads into chunks so the grid holds >= 8192 waves (32 per CU)
   // when the position count alone does not.
   const int64_t waves = (int64_t)p.B * p.n_groups;
-  int chunks = (int)((8192 + waves - 1) / waves);
+  int chunks = (int)((KFMI_ROWS_WAVES + waves - 1) / waves);
   chunks = chunks < 1 ? 1 : (chunks > H ? H : chunks);
   p.heads_per_chunk = (H + chunks - 1) / chunks;
   const int by = (H + p.heads_per_chunk - 1) / p.heads_per_chunk;
   const int bx = (int)((waves + 3) / 4);
+  p.rows_by = by;
+  p.vt_sblocks = (int)((a.S + 63) / 64);
+  p.vt_tiles = a.vt ? a.B * a.Hkv * p.vt_sblocks : 0;
+  if (a.vt && a.D != 128) return hipErrorInvalidValue;
   if (a.D == 128) return dispatch_rows<128>(p, a.style, a.rope, bx, by, stream);
   return dispatch_rows<256>(p, a.style, a.rope, bx, by, stream);
 }

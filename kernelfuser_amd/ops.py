@@ -56,21 +56,24 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 # Low-level launchers (caller-preallocated buffers, no checks beyond the C ABI's)
 # ---------------------------------------------------------------------------
 
-def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_norm=True, norm_style=None):
+def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_norm=True, norm_style=None, vt=None):
     """RMSNorm*gamma (+ rotate-half RoPE) of K rows into ``kn`` and, unless
     ``only_k``, of Q rows into ``qn`` in one launch (rope:652-658).
 
     ``inputs`` is the reference 7-tuple ``(q, k, v, gq, gk, cos, sin)``; with
     ``rope=False`` the table entries are ignored.  ``rows`` (Triton rows per
-    program) is ignored.
+    program) is ignored.  ``vt`` (optional, D=128, S % 8 == 0): the same launch
+    also writes V transposed per head into it (the V^T operand of
+    ``attention_prefill``).
     """
     q, k, v, gq, gk, cos, sin = inputs
     b, h, s, d = q.shape
     flags = (PREP_ONLY_K if only_k else 0) | (PREP_ROPE if rope else 0)
     _lib.call("kfmi_prepare_bf16",
-              None if only_k else ptr(q), ptr(k), None if only_k else ptr(gq), ptr(gk),
+              None if only_k else ptr(q), ptr(k), ptr(v) if vt is not None else None,
+              None if only_k else ptr(gq), ptr(gk),
               ptr(cos) if rope else None, ptr(sin) if rope else None,
-              None if only_k else ptr(qn), ptr(kn),
+              None if only_k else ptr(qn), ptr(kn), ptr(vt),
               b, h, k.shape[1], s, d, EPS, _style(norm_style, hf_norm), flags, stream_of(k))
 
 
@@ -247,7 +250,7 @@ def norm_rope(q, k, gq, gk, cos=None, sin=None, *, norm_style="fp32", qn=None, k
 def _norm_rope_into(q, k, gq, gk, cos, sin, qn, kn, norm_style):
     b, h, s, d = q.shape
     rope = cos is not None
-    _lib.call("kfmi_prepare_bf16", ptr(q), ptr(k), ptr(gq), ptr(gk), ptr(cos), ptr(sin), ptr(qn), ptr(kn),
+    _lib.call("kfmi_prepare_bf16", ptr(q), ptr(k), None, ptr(gq), ptr(gk), ptr(cos), ptr(sin), ptr(qn), ptr(kn), None,
               b, h, k.shape[1], s, d, EPS, NORM_STYLES[norm_style], PREP_ROPE if rope else 0, stream_of(q))
 
 

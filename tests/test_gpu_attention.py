@@ -172,3 +172,25 @@ def test_transpose_v_d256(gpu):
     transpose_v(v, vt)
     torch.cuda.synchronize()
     assert torch.equal(vt.view(2, 3, 256, 200), v.transpose(2, 3))
+
+
+@pytest.mark.parametrize("only_k,s", [(True, 1000), (False, 72), (True, 8)])
+def test_prepare_writes_vt(gpu, only_k, s):
+    """The preparation launch with a V^T output writes vt = V transposed per
+    head and leaves its row outputs bit-identical to the launch without it."""
+    from kernelfuser_amd import prepare_attention
+    xs = make_inputs(2, s, QWEN3_8B, 707).to(gpu)
+    qn1, kn1 = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    qn2, kn2 = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    vt = torch.full_like(xs.v, 3.0)
+    announce(f"prepare with vt only_k={only_k} S={s}")
+    prepare_attention(xs.reference7, qn1, kn1, only_k=only_k, norm_style="fp32")
+    prepare_attention(xs.reference7, qn2, kn2, only_k=only_k, norm_style="fp32", vt=vt)
+    torch.cuda.synchronize()
+    assert torch.equal(kn1, kn2)
+    if not only_k:
+        assert torch.equal(qn1, qn2)
+    assert torch.equal(vt.view(2, 8, 128, s), xs.v.transpose(2, 3))
+    with pytest.raises(ValueError):  # D=128 needs S % 8 == 0 for V^T rows
+        x2 = make_inputs(1, 12, QWEN3_8B, 1).to(gpu)
+        prepare_attention(x2.reference7, None, torch.empty_like(x2.k), only_k=True, vt=torch.empty_like(x2.v))
