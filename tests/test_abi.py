@@ -1,0 +1,117 @@
+"""The C-ABI library on a host without a GPU: it loads, reports its ABI
+version, exports every entry point ``include/kfmi.h`` declares, and rejects
+invalid arguments with KFMI_EINVAL and a message before touching a device.
+No compute call is made here."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernelfuser_amd import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "kfmi.h"
+EINVAL = _lib.KFMI_EINVAL
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(kfmi_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_declares_the_bound_entry_points():
+    names = _declared()
+    assert "kfmi_abi_version" in names and "kfmi_last_error" in names
+    assert set(_lib.SIGNATURES) == set(names) - {"kfmi_abi_version", "kfmi_last_error"}
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    m = re.search(r"#define KFMI_ABI_VERSION (\d+)", HEADER.read_text())
+    assert lib.kfmi_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
+
+
+def _err(lib):
+    return lib.kfmi_last_error().decode()
+
+
+# (entry point, arguments, fragment of the expected message); pointers are
+# NULL or a fake aligned value that is never dereferenced because an earlier
+# argument check fails first.
+FAKE = 1 << 20
+P = FAKE
+CASES = [
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, None, 0, 32, 8, 16, 128, 1e-6, 2, 2, None), "must be >= 1"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 64, 1e-6, 2, 2, None), "D must be"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, None, 1, 30, 8, 16, 128, 1e-6, 2, 2, None), "multiple of Hkv"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 7, 2, None), "norm_style"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 2, 64, None), "flags"),
+    ("kfmi_prepare_bf16", (P, None, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 2, 2, None), "k must not"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, None, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 2, 2, None), "cos"),
+    ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, P, 1, 32, 8, 16, 128, 1e-6, 2, 2, None), "v must not"),
+    ("kfmi_prepare_bf16", (P, P, P, P, P, P, P, P, P, P, 1, 32, 8, 12, 128, 1e-6, 2, 2, None), "S % 8"),
+    ("kfmi_prepare_bf16", (P + 2, P, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 2, 0, None), "aligned"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 33, 64, None), "bm"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 48, None), "bn"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, None, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None),
+     "both rotary"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.0, 1e-6, 1, 1, 2, 128, 64, None),
+     "scale"),
+    ("kfmi_attention_bf16", (P, P, P, None, None, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None),
+     "gq"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 2 ** 16, 8, 2 ** 12, 256, 0.1, 1e-6, 1, 1, 2, 128, 64,
+                             None), "2^31"),
+    ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 5, 2,
+                                    128, 64, None), "Invalid fusion mode"),
+    ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 0, 2,
+                                    128, 64, None), "Missing scratch buffers"),
+    ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2,
+                                    128, 64, None), "Missing scratch buffers"),
+    ("kfmi_transpose_v_bf16", (P, P, 4, 100, 128, None), "multiple of 8"),
+    ("kfmi_transpose_v_bf16", (P, P, 4, 64, 96, None), "D must be"),
+    ("kfmi_transpose_v_bf16", (P, None, 4, 64, 128, None), "vt must not"),
+    ("kfmi_factored_prepare_bf16", (P, P, P, P, None, P, 1, 16, 8, 16, 256, 1e-6, None), "inv must not"),
+    ("kfmi_factored_prepare_bf16", (P, P, P, P, P, P, 1, 16, 8, 16, 256, -1.0, None), "eps"),
+    ("kfmi_factored_attention_bf16", (P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 2, 128, 64, None), "inv_mode"),
+    ("kfmi_factored_attention_bf16", (P, P, P, None, P, 1, 16, 8, 16, 256, 1e-6, 1, 0, 128, 64, None),
+     "inv must not"),
+    ("kfmi_factored_attention_bf16", (P, P, P, P + 2, P, 1, 16, 8, 16, 256, 1e-6, 1, 1, 128, 64, None), "4-byte"),
+    ("kfmi_launch_factored_attention_bf16", (P, P, P, P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 128, 16, None),
+     "bn"),
+]
+
+
+@pytest.mark.parametrize("name,args,fragment", CASES, ids=[f"{c[0]}-{i}" for i, c in enumerate(CASES)])
+def test_invalid_arguments_fail_before_launch(lib, name, args, fragment):
+    rc = getattr(lib, name)(*args)
+    assert rc == EINVAL, (rc, _err(lib))
+    assert fragment in _err(lib), _err(lib)
+
+
+def test_call_maps_einval_to_value_error(lib):
+    with pytest.raises(ValueError, match="Invalid fusion mode"):
+        _lib.call("kfmi_launch_attention_bf16", P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1,
+                  1e-6, 1, 9, 2, 128, 64, None)
+
+
+def test_last_error_is_per_thread(lib):
+    import threading
+    lib.kfmi_transpose_v_bf16(P, P, 4, 100, 128, None)
+    seen = {}
+
+    def other():
+        seen["msg"] = lib.kfmi_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == "" and "multiple of 8" in _err(lib)
