@@ -26,9 +26,14 @@
 //          v_permlane32_swap with the other half-wave, and the per-query
 //          rescale of O is a per-lane scalar;
 //   GEMM2  O^T = V^T . P^T A = V^T read from the row-major V tile in LDS with
-//                               ds_read_b64_tr_b16 (transpose on read),
+//                               ds_read_b64_tr_b16 (transpose on read), or,
+//                               when the caller supplies V transposed per head
+//                               (written by the preparation launch), from a
+//                               V^T tile with one ds_read_b128 per operand,
 //                           B = P^T straight from the GEMM1 accumulator
-//                               (exp2, cvt to bf16, no data movement).
+//                               (exp2, cvt to bf16, no data movement; with
+//                               V^T the keys of each 16-key step are put in
+//                               consecutive order by one v_permlane32_swap).
 // MFMA: v_mfma_f32_32x32x16_bf16.  Operand layouts: A[m][k] -> lane
 // m + 32*(k/8), element k%8; B[k][n] -> lane n + 32*(k/8), element k%8;
 // C[m][n] -> lane n + 32*((m/4)%2), register (m/8)*4 + m%4.
