@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 3
+#define KFMI_ABI_VERSION 4
 
 /* status codes */
 #define KFMI_OK 0
@@ -52,6 +52,7 @@ extern "C" {
 /* mode of kfmi_launch_attention_bf16 (rope:668) */
 #define KFMI_MODE_QUERY 0   /* K prepared once, Q norm(+RoPE) in the attention prologue */
 #define KFMI_MODE_UNFUSED 1 /* Q and K prepared, plain attention */
+#define KFMI_MODE_FULL 2    /* one launch: Q and K norm(+RoPE) inside attention, K per key tile */
 
 /* Version of this ABI (KFMI_ABI_VERSION). */
 int kfmi_abi_version(void);
@@ -93,9 +94,12 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
 
 /* The launches of launch_attention (rope:661-677): mode QUERY prepares K
  * into kn (K rows only) then runs attention with the fused Q prologue; mode
- * UNFUSED prepares Q into qn and K into kn, then runs plain attention.  gk is
- * K's gamma.  Scratch kn (and qn for UNFUSED) is caller-allocated, as the
- * reference requires (rope:665-672).  cos/sin NULL disables RoPE.
+ * UNFUSED prepares Q into qn and K into kn, then runs plain attention; mode
+ * FULL is one launch in which attention normalises (and rotates) Q in its
+ * prologue and every K tile as it uses it (FUSE_Q and FUSE_K, rope:619-635;
+ * qn, kn and vt are unused and may be NULL).  gk is K's gamma.  Scratch kn
+ * (and qn for UNFUSED) is caller-allocated, as the reference requires
+ * (rope:665-672).  cos/sin NULL disables RoPE.
  * vt (optional, may be NULL): caller-allocated scratch of V's size; when
  * given and D == 128, Hq/Hkv is even and S % 8 == 0, the preparation launch
  * also writes V transposed per head ([B,Hkv,D,S]) and the attention kernel

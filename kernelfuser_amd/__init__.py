@@ -7,12 +7,18 @@ PyTorch-ROCm ops with the signatures of KernelFuser's attention-prologue path:
 * ``launch_attention`` / ``prepare_attention``  (rope:652-677)
 * ``launch_factored_attention``  (src/e1_qk_publication_v3.py:641-652)
 * ``norm_rope``  isolated per-head Q/K RMSNorm + RoPE
+* ``fused`` / ``anchor`` / ``separate``, ``model_scale``  (the older API, rope:25-36, :185-212)
 
 Build the native library with ``python -m kernelfuser_amd.build``.
 """
 from .ops import (  # noqa: F401
     EPS,
+    MODEL_QUERY_PRE_ATTN_SCALAR,
     MODELS,
+    anchor,
+    fused,
+    model_scale,
+    separate,
     attention_flops,
     attention_prefill,
     factored_attention,
@@ -31,7 +37,8 @@ from .ops import (  # noqa: F401
 from .inputs import GEMMA3_12B, QWEN3_8B, Inputs, make_inputs, rope_tables  # noqa: F401
 
 __all__ = [
-    "EPS", "MODELS", "optimized_attention", "attention_prefill", "launch_attention", "prepare_attention",
+    "EPS", "MODELS", "MODEL_QUERY_PRE_ATTN_SCALAR", "model_scale", "fused", "anchor", "separate",
+    "optimized_attention", "attention_prefill", "launch_attention", "prepare_attention",
     "launch_factored_attention", "prepare_factored", "factored_attention", "factored_qk_attention",
     "norm_rope", "uses_vt", "transpose_v", "attention_flops", "norm_rope_bytes", "k_prep_bytes", "make_inputs", "rope_tables",
     "Inputs", "QWEN3_8B", "GEMMA3_12B",

@@ -14,12 +14,12 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
 PREP_ONLY_K, PREP_ROPE = 1, 2
-MODE_QUERY, MODE_UNFUSED = 0, 1
+MODE_QUERY, MODE_UNFUSED, MODE_FULL = 0, 1, 2
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64

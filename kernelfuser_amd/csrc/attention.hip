@@ -71,6 +71,7 @@ namespace {
 
 struct AttnParams {
   const uint16_t *q, *k, *v, *gq, *cos, *sin;
+  const uint16_t *gk;  // K's gamma for the per-tile K prologue (mode 'full'), else NULL
   const uint16_t *vt;  // V transposed per head ([B,Hkv,D,S]) for the VT kernels
   uint16_t *out;
   float *inv;
@@ -434,6 +435,81 @@ __device__ __forceinline__ void gemm1(const unsigned char *smem, int kbuf, const
   }
 }
 
+// GEMM1 with the K prologue of mode 'full' (rope:630-631, FUSE_K): the lane's
+// raw K row chunks are read from the tile (row 32*kb + lr: columns 16c + 8g ..
+// +7 for every c, both rotate-half partners d and d +/- D/2 in this lane),
+// RMSNorm * gamma_k (+ RoPE at the key's position) is applied in FP32 with the
+// style's rounding points, rounded to BF16, and the MFMAs use the result.
+// The RMS needs one cross-half sum.  Keys past S are zero rows (their table
+// row is clamped to 0); they are masked later.  Every wave recomputes the
+// tile's rows, as every program of the reference does.
+template <int D, int BN, int ST, bool ROPE>
+__device__ __forceinline__ void gemm1_fused_k(const unsigned char *smem, int kbuf, const uint32_t (&kra)[8],
+                                              const bf16x8_t (&qreg)[D / 16], f32x16_t (&s)[BN / 32],
+                                              const AttnParams &p, int key0, int g, int lr) {
+  constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16, HC = NC / 2;
+  auto chunk = [&](int kb, int c) -> u32x4_t {
+    return *reinterpret_cast<const u32x4_t *>(smem + kbuf + kb * 32 * RB + kra[c & 7] + (c >> 3) * 256);
+  };
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    // pass 1: sum of squares of the row (chunks re-read in pass 2 instead of
+    // being held, to keep the register footprint of the loop)
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8];
+      unpack8(chunk(kb, c), x);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) ss = __fmaf_rn(x[jj], x[jj], ss);
+    }
+    ss = sum_halves(ss);
+    const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+    const int key = key0 + 32 * kb + lr;
+    const int64_t trow = key < p.S ? (int64_t)key * D : 0;
+    // pass 2: one rotate-half pair (c, c + D/32 chunks) at a time; the MFMAs
+    // accumulate in chunk order 0 .. NC-1, as in gemm1.
+    bf16x8_t khi[HC];
+    s[kb] = f32x16_t{};
+#pragma unroll
+    for (int c = 0; c < HC; ++c) {
+      const int c2 = c + HC;
+      float x1[8], x2[8], g1[8], g2[8], n1[8], n2[8], y1[8], y2[8];
+      unpack8(chunk(kb, c), x1);
+      unpack8(chunk(kb, c2), x2);
+      unpack8(ld16(p.gk + 16 * c + 8 * g), g1);
+      unpack8(ld16(p.gk + 16 * c2 + 8 * g), g2);
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        n1[jj] = norm_elem<ST>(x1[jj], inv, g1[jj]);
+        n2[jj] = norm_elem<ST>(x2[jj], inv, g2[jj]);
+      }
+      if constexpr (ROPE) {
+        float cs1[8], sn1[8], cs2[8], sn2[8];
+        unpack8(ld16(p.cos + trow + 16 * c + 8 * g), cs1);
+        unpack8(ld16(p.sin + trow + 16 * c + 8 * g), sn1);
+        unpack8(ld16(p.cos + trow + 16 * c2 + 8 * g), cs2);
+        unpack8(ld16(p.sin + trow + 16 * c2 + 8 * g), sn2);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          y1[jj] = rope_elem<ST>(n1[jj], n2[jj], cs1[jj], sn1[jj], true);
+          y2[jj] = rope_elem<ST>(n2[jj], n1[jj], cs2[jj], sn2[jj], false);
+        }
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) { y1[jj] = n1[jj]; y2[jj] = n2[jj]; }
+      }
+      s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(pack8(y1)), qreg[c], s[kb], 0, 0, 0);
+      khi[c] = as_bf16x8(pack8(y2));
+      // one pair at a time: the scheduler would otherwise hoist every table
+      // load of the tile and run out of registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int c = 0; c < HC; ++c) s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(khi[c], qreg[c + HC], s[kb], 0, 0, 0);
+  }
+}
+
 // GEMM2: O^T[d][query] += V^T . P^T for the V tile at LDS byte vbuf; the A
 // operand's slot j of half g is key 16*c2 + 8*(j/4) + 4*g + j%4, matching the
 // P^T registers of Softmax::step.
@@ -722,8 +798,10 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 // ---------------------------------------------------------------------------
 // General kernel: one head, 4 waves x 32 rows, D in {128, 256}.
 // ---------------------------------------------------------------------------
-template <int D, int BN, bool CAUSAL, int PRO, int ST>
+template <int D, int BN, bool CAUSAL, int PRO, int ST, bool FK = false>
 __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnParams p) {
+  // FK: K arrives raw and every tile gets the K prologue of mode 'full'.
+  static_assert(!FK || PRO == PRO_NORM || PRO == PRO_NORM_ROPE, "mode 'full' fuses Q as well");
   constexpr int BM = 128;            // query rows per workgroup (4 waves x 32)
   constexpr int RB = 2 * D;          // bytes per K/V row
   constexpr int TILE = BN * RB;      // bytes per K or V tile
@@ -831,7 +909,12 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     __syncthreads();
     if (t + 2 < nT) copy_k(t + 2, KFREE);
     if (t + 1 < nT) copy_v(t + 1, VFREE);
-    if (t + 1 < nTw) gemm1<D, BN>(smem, KNEXT, kra, qreg, nxt);
+    if (t + 1 < nTw) {
+      if constexpr (FK)
+        gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, KNEXT, kra, qreg, nxt, p, (t + 1) * BN, g, lr);
+      else
+        gemm1<D, BN>(smem, KNEXT, kra, qreg, nxt);
+    }
     if (t < nTw) {
       bf16x8_t pb[NK16];
       sm.step(cur, t, q0, qrow, S, g, cl, o, pb);
@@ -842,7 +925,12 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   f32x16_t sa[NKB], sb[NKB];
   wait_copies();
   __syncthreads();
-  if (nTw > 0) gemm1<D, BN>(smem, K0, kra, qreg, sa);
+  if (nTw > 0) {
+    if constexpr (FK)
+      gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, K0, kra, qreg, sa, p, 0, g, lr);
+    else
+      gemm1<D, BN>(smem, K0, kra, qreg, sa);
+  }
   for (int t = 0;;) {
     iteration(std::integral_constant<int, 0>{}, t, sa, sb);
     if (++t >= nT) break;
@@ -855,6 +943,12 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
 
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
 hipError_t launch_t(const AttnParams &p, bool pp, int blocks, hipStream_t s) {
+  if constexpr (PRO == PRO_NORM || PRO == PRO_NORM_ROPE) {
+    if (p.gk) {  // mode 'full': general kernel with the per-tile K prologue
+      hipLaunchKernelGGL((attn_fwd_kernel<D, BN, CAUSAL, PRO, ST, true>), dim3(blocks), dim3(256), 0, s, p);
+      return hipGetLastError();
+    }
+  }
   if constexpr (D == 128) {
     if (pp) {
       if (p.vt)
@@ -892,6 +986,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   constexpr double LOG2E = 1.4426950408889634;
   AttnParams p;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
+  p.gk = a.gk;
   p.out = a.out; p.inv = a.inv;
   p.vt = nullptr;
   p.S = a.S;
@@ -903,7 +998,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int BM = 128;
   p.n_qblocks = (int)((a.S + BM - 1) / BM);
   const int G = p.Hq / p.Hkv;
-  const bool pp = a.D == 128 && G % 2 == 0;
+  const bool pp = a.D == 128 && G % 2 == 0 && a.gk == nullptr;  // mode 'full' runs the general kernel
   if (pp && a.vt && a.S % 8 == 0) p.vt = a.vt;  // V^T rows must be 16-byte aligned
   int blocks;
   if (pp) {

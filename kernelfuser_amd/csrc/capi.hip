@@ -128,12 +128,13 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *g
 }
 
 static int attention_impl(const void *q, const void *k, const void *v, const void *vt, const void *gq,
-                          const void *cos, const void *sin, void *out, float *inv, int64_t B, int64_t Hq,
+                          const void *gk, const void *cos, const void *sin, void *out, float *inv, int64_t B, int64_t Hq,
                           int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal, int prologue,
                           int style, int bm, int bn, hipStream_t stream) {
   kfmi::AttnArgs a{};
   a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.v = (const uint16_t *)v; a.gq = (const uint16_t *)gq;
   a.vt = (const uint16_t *)vt;
+  a.gk = (const uint16_t *)gk;
   a.cos = (const uint16_t *)cos; a.sin = (const uint16_t *)sin; a.out = (uint16_t *)out; a.inv = inv;
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
   a.causal = causal != 0; a.prologue = prologue; a.style = style; a.scale = scale; a.eps = eps;
@@ -156,7 +157,7 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
   KFMI_TRY(check_device());
   const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
-  return attention_impl(q, k, v, vt, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
+  return attention_impl(q, k, v, vt, gq, nullptr, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
                         style_of(norm_style), bm, bn, (hipStream_t)stream);
 }
 
@@ -167,8 +168,18 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
   KFMI_TRY(check_tiles(bm, bn));
-  if (mode != KFMI_MODE_QUERY && mode != KFMI_MODE_UNFUSED) return fail(KFMI_EINVAL, "Invalid fusion mode %d", mode);
+  if (mode != KFMI_MODE_QUERY && mode != KFMI_MODE_UNFUSED && mode != KFMI_MODE_FULL)
+    return fail(KFMI_EINVAL, "Invalid fusion mode %d", mode);
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}}));
+  if (mode == KFMI_MODE_FULL) {  // one launch, K normalised per tile; no scratch (rope:671-677)
+    if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
+    if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
+    if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
+    KFMI_TRY(check_device());
+    return attention_impl(q, k, v, nullptr, gq, gk, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal,
+                          cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM, style_of(norm_style), bm, bn,
+                          (hipStream_t)stream);
+  }
   if (kn == nullptr || (mode == KFMI_MODE_UNFUSED && qn == nullptr)) return fail(KFMI_EINVAL, "Missing scratch buffers");
   KFMI_TRY(check_ptrs({{kn, "kn"}}));
   if (mode == KFMI_MODE_UNFUSED) KFMI_TRY(check_ptrs({{qn, "qn"}}));
@@ -194,7 +205,7 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   if (e != hipSuccess) return launch_status(e, "prepare launch");
   const bool query = mode == KFMI_MODE_QUERY;
   const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
-  return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, cos, sin, out, nullptr, B, Hq, Hkv, S, D,
+  return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, nullptr, cos, sin, out, nullptr, B, Hq, Hkv, S, D,
                         scale, eps, causal, pro, style_of(norm_style), bm, bn, (hipStream_t)stream);
 }
 
@@ -234,7 +245,7 @@ int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, f
   if (inv && (reinterpret_cast<uintptr_t>(inv) & 3u)) return fail(KFMI_EINVAL, "inv must be 4-byte aligned");
   KFMI_TRY(check_device());
   const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
-  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
                         kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
 }
 
@@ -253,7 +264,7 @@ int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void
   r.only_k = true; r.rope = false; r.style = kfmi::ST_FACTORED; r.eps = eps;
   hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, "factored prepare launch");
-  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
+  return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
                         kfmi::PRO_FACTORED_CALC, kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
 }
 

@@ -37,6 +37,7 @@ struct RowsArgs {
 
 struct AttnArgs {
   const uint16_t *q, *k, *v, *gq, *cos, *sin;
+  const uint16_t *gk;  // mode 'full': K is raw and normalised (+RoPE) per tile with this gamma; else NULL
   const uint16_t *vt;  // V transposed per head ([B,Hkv,D,S]) or NULL
   uint16_t *out;
   float *inv;

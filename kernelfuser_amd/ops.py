@@ -17,12 +17,13 @@ Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import math
 from typing import Optional
 
 import torch
 
 from . import _lib
-from ._lib import MODE_QUERY, MODE_UNFUSED, NORM_STYLES, PREP_ONLY_K, PREP_ROPE, ptr, stream_of
+from ._lib import MODE_FULL, MODE_QUERY, MODE_UNFUSED, NORM_STYLES, PREP_ONLY_K, PREP_ROPE, ptr, stream_of
 
 EPS = 1e-6  # rope:32; the reference kernels hard-code it (rope:558)
 
@@ -34,6 +35,18 @@ MODELS = {
     "Gemma-3-4B": (8, 4, 256), "Gemma-3-12B": (16, 8, 256),
     "Gemma-3-27B": (32, 16, 128),
 }
+
+# Gemma-3 checkpoints set query_pre_attn_scalar = 256, also for the D=128
+# 27B geometry; Qwen3 scales by D^-1/2 (rope:25-36).
+MODEL_QUERY_PRE_ATTN_SCALAR = {"Gemma-3-4B": 256.0, "Gemma-3-12B": 256.0, "Gemma-3-27B": 256.0}
+
+
+def model_scale(name: str, d: int) -> float:
+    """Attention scale of a model (rope:34-36): query_pre_attn_scalar^-1/2 when
+    the model sets one, else D^-1/2."""
+    scalar = MODEL_QUERY_PRE_ATTN_SCALAR.get(name)
+    return float(1.0 / math.sqrt(scalar if scalar is not None else d))
+
 
 _arch_cache: dict[int, str] = {}
 
@@ -56,7 +69,8 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 # Low-level launchers (caller-preallocated buffers, no checks beyond the C ABI's)
 # ---------------------------------------------------------------------------
 
-def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_norm=True, norm_style=None, vt=None):
+def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_norm=True, norm_style=None, vt=None,
+                      eps=EPS):
     """RMSNorm*gamma (+ rotate-half RoPE) of K rows into ``kn`` and, unless
     ``only_k``, of Q rows into ``qn`` in one launch (rope:652-658).
 
@@ -74,7 +88,7 @@ def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_nor
               None if only_k else ptr(gq), ptr(gk),
               ptr(cos) if rope else None, ptr(sin) if rope else None,
               None if only_k else ptr(qn), ptr(kn), ptr(vt),
-              b, h, k.shape[1], s, d, EPS, _style(norm_style, hf_norm), flags, stream_of(k))
+              b, h, k.shape[1], s, d, float(eps), _style(norm_style, hf_norm), flags, stream_of(k))
 
 
 def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, warps=4, stages=1,
@@ -83,8 +97,11 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
 
     ``mode='query'``: K is prepared once into ``kn``; Q's norm (+RoPE) runs in the
     attention prologue.  ``mode='unfused'``: Q into ``qn`` and K into ``kn``, then
-    plain attention.  Scratch buffers must be preallocated (rope:665-672).  Timings
-    must include every launch, as this function issues them.
+    plain attention.  ``mode='full'``: one launch; attention normalises (and
+    rotates) Q in its prologue and each K tile as it uses it -- no scratch, same
+    values as ``'query'``.  Scratch buffers must be preallocated for the other
+    modes (rope:665-672).  Timings must include every launch, as this function
+    issues them.
 
     ``vt`` (optional, shaped like V): scratch for V transposed per head.  When
     given (and D=128, an even GQA ratio and S % 8 == 0), the preparation launch
@@ -93,11 +110,7 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
     """
     if mode not in ("full", "query", "unfused"):
         raise ValueError("Invalid fusion mode")
-    if mode == "full":
-        raise NotImplementedError(
-            "mode='full' (K norm+RoPE recomputed per key tile) is not provided by the gfx950 "
-            "library; use 'query' (K prepared once) or 'unfused'")
-    if kn is None or (mode == "unfused" and qn is None):
+    if mode != "full" and (kn is None or (mode == "unfused" and qn is None)):
         raise ValueError("Missing scratch buffers")
     q, k, v, gq, gk, cos, sin = inputs
     b, h, s, d = q.shape
@@ -106,12 +119,12 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
               ptr(cos) if rope else None, ptr(sin) if rope else None,
               ptr(out), ptr(qn), ptr(kn), ptr(vt),
               b, h, k.shape[1], s, d, float(d) ** -0.5, EPS, int(bool(causal)),
-              MODE_QUERY if mode == "query" else MODE_UNFUSED, _style(norm_style, hf_norm),
+              {"query": MODE_QUERY, "unfused": MODE_UNFUSED, "full": MODE_FULL}[mode], _style(norm_style, hf_norm),
               _bm(bm), _bn(bn), stream_of(q))
 
 
 def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=False, fuse_q=True,
-                      norm_style="fp32", bm=128, bn=64, scale=None, vt=None):
+                      norm_style="fp32", bm=128, bn=64, scale=None, vt=None, eps=EPS):
     """The attention launch alone (attention_v2_kernel, rope:608-649) on a prepared
     ``kn``.  ``fuse_q=True``: raw ``q`` with its RMSNorm (``gq``) and, when both
     tables are given, RoPE in the prologue (FUSE_Q); ``fuse_q=False``: ``q`` is
@@ -120,7 +133,7 @@ def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=Fals
     shape allows it (``uses_vt``)."""
     b, h, s, d = q.shape
     _lib.call("kfmi_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(vt), ptr(gq), ptr(cos), ptr(sin), ptr(out),
-              b, h, kn.shape[1], s, d, float(d) ** -0.5 if scale is None else float(scale), EPS,
+              b, h, kn.shape[1], s, d, float(d) ** -0.5 if scale is None else float(scale), float(eps),
               int(bool(causal)), int(bool(fuse_q)), NORM_STYLES[norm_style], _bm(bm), _bn(bn), stream_of(q))
 
 
@@ -219,6 +232,79 @@ def optimized_attention(q, k, v, gq, gk, cos=None, sin=None, *, causal=False, mo
     if max(q.numel(), k.numel()) >= 2 ** 31:
         raise ValueError("Tensors must have fewer than 2**31 elements")
     return torch.ops.kfmi.optimized_attention(q, k, v, gq, gk, cos, sin, bool(causal), mode, int(bn), norm_style)
+
+
+def _position_table(t, q):
+    """[S,D], [B,S,D] or [B,1,S,D] rotary table -> contiguous [S,D] of q's dtype.
+    All rows of the isolated workloads share positions, so the first broadcast
+    slice is exact (rope:193-200)."""
+    if t.ndim == 4:
+        t = t[:, 0]
+    if t.ndim == 3:
+        t = t[0]
+    return t.to(q.dtype).contiguous()
+
+
+def _fused_checks(q, k, v, gq, gk, cos, sin):
+    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
+        raise ValueError("Expected q [B,Hq,S,D] and k, v [B,Hkv,S,D]")
+    b, h, s, d = q.shape
+    if d not in (128, 256) or k.shape[0] != b or tuple(k.shape[2:]) != (s, d) or h % k.shape[1]:
+        raise ValueError("Expected D in (128, 256), matching batch and sequence, and Hq a multiple of Hkv")
+    tensors = (q, k, v) + tuple(t for t in (gq, gk, cos, sin) if t is not None)
+    _check_device(tensors, q.device)
+
+
+def fused(q, k, v, gq, gk, cos, sin, causal, eps=EPS, scale=None, norm_style="qwen3"):
+    """Fused Q/K RMSNorm + rotate-half RoPE + attention with explicit ``eps`` and
+    ``scale`` (the older API, rope:185-203; ``scale=None`` is D^-1/2).
+
+    The HF/Qwen3 rounding chain (``norm_style='qwen3'``, the reference's only
+    style here; ``'hf'`` is accepted as its name in this package) is applied to
+    both Q and K.  The reference recomputes K's norm+RoPE for every key tile
+    inside one kernel; here K is prepared once (one launch) and Q's
+    norm+RoPE runs in the attention prologue -- the same values, since a K row
+    prepared once or per tile is the same function of the same inputs.
+    Tables may be [S,D], [B,S,D] or [B,1,S,D] (the first broadcast slice is
+    used, rope:193-200)."""
+    if norm_style not in ("qwen3", "hf"):
+        raise ValueError("fused implements the HF/Qwen3 norm_style only")
+    cos, sin = _position_table(cos, q), _position_table(sin, q)
+    _fused_checks(q, k, v, gq, gk, cos, sin)
+    b, h, s, d = q.shape
+    if tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d):
+        raise ValueError("Expected rotary tables of S rows")
+    out, kn = torch.empty_like(q), torch.empty_like(k)
+    vt = torch.empty_like(v) if uses_vt(h, k.shape[1], s, d) else None
+    with torch.cuda.device(q.device):
+        prepare_attention((q, k, v, gq, gk, cos, sin), None, kn, only_k=True, rope=True, norm_style="hf", vt=vt,
+                          eps=eps)
+        attention_prefill(q, kn, v, out, gq=gq, cos=cos, sin=sin, causal=causal, fuse_q=True, norm_style="hf",
+                          scale=scale, vt=vt, eps=eps)
+    return out
+
+
+def anchor(q, k, v, cos, sin, causal, scale=None):
+    """Attention on already prepared Q/K (the reference's FUSED=False launch,
+    rope:205-208); the tables are unused."""
+    _fused_checks(q, k, v, None, None, None, None)
+    out = torch.empty_like(q)
+    with torch.cuda.device(q.device):
+        attention_prefill(q, k, v, out, causal=causal, fuse_q=False, scale=scale)
+    return out
+
+
+def separate(q, k, v, gq, gk, cos, sin, causal, eps=EPS, scale=None, norm_style="qwen3"):
+    """Separate preparation of Q and K (HF/Qwen3 chain, one launch) followed by
+    ``anchor`` (rope:210-212)."""
+    if norm_style not in ("qwen3", "hf"):
+        raise ValueError("separate implements the HF/Qwen3 norm_style only")
+    cos, sin = _position_table(cos, q), _position_table(sin, q)
+    _fused_checks(q, k, v, gq, gk, cos, sin)
+    qn, kn = torch.empty_like(q), torch.empty_like(k)
+    with torch.cuda.device(q.device):
+        prepare_attention((q, k, v, gq, gk, cos, sin), qn, kn, only_k=False, rope=True, norm_style="hf", eps=eps)
+    return anchor(qn, kn, v, cos, sin, causal, scale)
 
 
 def norm_rope(q, k, gq, gk, cos=None, sin=None, *, norm_style="fp32", qn=None, kn=None):

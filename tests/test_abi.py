@@ -72,6 +72,10 @@ CASES = [
                              None), "2^31"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 5, 2,
                                     128, 64, None), "Invalid fusion mode"),
+    ("kfmi_launch_attention_bf16", (P, P, P, P, None, P, P, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 2,
+                                    2, 128, 64, None), "gk must not"),
+    ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, None, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 2,
+                                    2, 128, 64, None), "both rotary"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 0, 2,
                                     128, 64, None), "Missing scratch buffers"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2,

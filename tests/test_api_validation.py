@@ -6,6 +6,8 @@ launchers raise 'Invalid fusion mode' / 'Missing scratch buffers'
 (rope:668-672).  A valid call on CPU tensors stops at the device rule, so
 each case below is checked against the message of the rule it breaks.
 """
+import math
+
 import pytest
 import torch
 
@@ -98,8 +100,9 @@ def test_launcher_mode_and_scratch(xs):
         kf.launch_attention(xs.reference7, out, mode="query")
     with pytest.raises(ValueError, match="Missing scratch buffers"):
         kf.launch_attention(xs.reference7, out, mode="unfused", kn=torch.empty_like(xs.k))
-    with pytest.raises(NotImplementedError):
-        kf.launch_attention(xs.reference7, out, mode="full", kn=torch.empty_like(xs.k))
+    # mode 'full' needs no scratch: on CPU tensors it reaches the library, whose
+    # pointer/device checks reject host memory only after argument validation
+    # (so no ValueError about scratch is raised here)
 
 
 def test_norm_rope_rules(xs):
@@ -116,3 +119,28 @@ def test_factored_rules(xs):
         kf.factored_qk_attention(xs.q, xs.k, xs.v[:, :1], xs.gq, xs.gk)
     with pytest.raises(ValueError, match="contiguous BF16"):
         kf.factored_qk_attention(xs.q, xs.k, xs.v, xs.gq, xs.gk)
+
+
+def test_model_scale_and_tables():
+    from kernelfuser_amd import model_scale, MODELS
+    from kernelfuser_amd.ops import _position_table
+    assert model_scale("Qwen3-8B", 128) == 1.0 / math.sqrt(128)
+    assert model_scale("Gemma-3-27B", 128) == 1 / 16  # query_pre_attn_scalar 256 (rope:25-36)
+    assert model_scale("Gemma-3-4B", 256) == 1 / 16
+    assert set(MODELS) >= {"Qwen3-8B", "Gemma-3-12B", "Qwen3-30B-A3B"}
+    q = torch.zeros(2, 4, 8, 128, dtype=torch.bfloat16)
+    t = torch.arange(8 * 128, dtype=torch.float32).view(8, 128)
+    for shaped in (t, t[None].expand(2, -1, -1), t[None, None].expand(2, 1, -1, -1)):
+        got = _position_table(shaped, q)
+        assert got.shape == (8, 128) and got.dtype == torch.bfloat16 and got.is_contiguous()
+        assert torch.equal(got, t.to(torch.bfloat16))
+
+
+def test_fused_rules(xs):
+    import kernelfuser_amd as kf
+    with pytest.raises(ValueError, match="norm_style"):
+        kf.fused(xs.q, xs.k, xs.v, xs.gq, xs.gk, xs.cos, xs.sin, True, norm_style="legacy")
+    with pytest.raises(ValueError, match="contiguous BF16"):
+        kf.fused(xs.q, xs.k, xs.v, xs.gq, xs.gk, xs.cos, xs.sin, True)
+    with pytest.raises(ValueError, match="Expected q"):
+        kf.anchor(xs.q, xs.k, xs.v[:, :, :3], None, None, True)

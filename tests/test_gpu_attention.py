@@ -194,3 +194,30 @@ def test_prepare_writes_vt(gpu, only_k, s):
     with pytest.raises(ValueError):  # D=128 needs S % 8 == 0 for V^T rows
         x2 = make_inputs(1, 12, QWEN3_8B, 1).to(gpu)
         prepare_attention(x2.reference7, None, torch.empty_like(x2.k), only_k=True, vt=torch.empty_like(x2.v))
+
+
+@pytest.mark.parametrize("geom,b,s,causal,style,rope", [
+    (QWEN3_8B, 1, 129, True, "hf", True), (QWEN3_8B, 2, 200, False, "fp32", True),
+    ((8, 4, 256), 1, 65, True, "legacy", True), ((16, 8, 256), 1, 96, False, "fp32", False),
+    ((32, 4, 128), 1, 70, True, "fp32", False),
+])
+def test_mode_full(gpu, geom, b, s, causal, style, rope):
+    """mode='full' (one launch; Q and every K tile normalised inside attention,
+    rope:619-635, :668-677) passes the oracle gate and stays close to
+    mode='query': K may differ by one BF16 rounding (its row RMS is summed in
+    another order), and for the FP32 style the query path folds the logit
+    scale into Q before Q's single rounding while the general kernel rounds Q
+    unscaled."""
+    xs = make_inputs(b, s, geom, 808, rope=rope).to(gpu)
+    out_f, out_q, kn = torch.empty_like(xs.q), torch.empty_like(xs.q), torch.empty_like(xs.k)
+    announce(f"mode full {geom} B={b} S={s} causal={causal} {style} rope={rope}")
+    launch_attention(xs.reference7, out_f, causal=causal, mode="full", rope=rope, norm_style=style)
+    launch_attention(xs.reference7, out_q, causal=causal, mode="query", rope=rope, kn=kn, norm_style=style)
+    torch.cuda.synchronize()
+    cpu = [t.cpu() if t is not None else None for t in xs.astuple()]
+    ref = oracle.oracle_fp32(*cpu, causal)  # every style is gated against the FP32 oracle
+    assert oracle.attention_gate(out_f.cpu(), ref)["pass"]
+    # the two modes are two numerical paths, each within the gate of the oracle
+    d = (out_f.float() - out_q.float()).abs()
+    assert float(d.max()) <= 2e-2, float(d.max())
+    assert float(d.mean()) <= 1e-3, float(d.mean())
