@@ -101,7 +101,8 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
  * (and qn for UNFUSED) is caller-allocated, as the reference requires
  * (rope:665-672).  cos/sin NULL disables RoPE.
  * vt (optional, may be NULL): caller-allocated scratch of V's size; when
- * given and D == 128, Hq/Hkv is even and S % 8 == 0, the preparation launch
+ * given and D == 128, Hq/Hkv is even, S > 2944 (the shapes that run the
+ * ping-pong kernel) and S % 8 == 0, the preparation launch
  * also writes V transposed per head ([B,Hkv,D,S]) and the attention kernel
  * reads that instead of V (one 16-byte LDS read per V operand instead of two
  * transposing 8-byte reads).  Results are identical either way; the call

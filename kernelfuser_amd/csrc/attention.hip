@@ -982,6 +982,16 @@ hipError_t dispatch_pro(const AttnParams &p, int pro, int st, bool pp, int block
 
 }  // namespace
 
+// The ping-pong kernel needs D = 128 and an even GQA ratio, and pays off from
+// 24 query blocks of 128 rows (S > 2944): below that, 2-4 tile rounds per
+// CU leave its 8-wave workgroups unbalanced and the general kernel (two
+// 4-wave workgroups per CU) is faster (measured on MI355X: S=2048 causal
+// 50.8 vs 56.9 us, B=4 S=1000 53.1 vs 56.8 us; S=4096 145 vs 134 us).
+bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D) {
+  constexpr int64_t PP_MIN_QBLOCKS = 24;
+  return D == 128 && (Hq / Hkv) % 2 == 0 && (S + 127) / 128 >= PP_MIN_QBLOCKS;
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   constexpr double LOG2E = 1.4426950408889634;
   AttnParams p;
@@ -998,7 +1008,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   const int BM = 128;
   p.n_qblocks = (int)((a.S + BM - 1) / BM);
   const int G = p.Hq / p.Hkv;
-  const bool pp = a.D == 128 && G % 2 == 0 && a.gk == nullptr;  // mode 'full' runs the general kernel
+  const bool pp = attention_uses_pp(a.Hq, a.Hkv, a.S, a.D) && a.gk == nullptr;  // mode 'full': general kernel
   if (pp && a.vt && a.S % 8 == 0) p.vt = a.vt;  // V^T rows must be 16-byte aligned
   int blocks;
   if (pp) {

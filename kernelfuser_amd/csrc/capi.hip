@@ -189,9 +189,8 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_device());
   const bool rope = cos != nullptr;
-  // V^T is used by the D=128 ping-pong kernel (even GQA ratio) when its rows
-  // are 16-byte aligned.
-  const bool use_vt = vt != nullptr && D == 128 && (Hq / Hkv) % 2 == 0 && S % 8 == 0;
+  // V^T is used by the ping-pong kernel when its rows are 16-byte aligned.
+  const bool use_vt = vt != nullptr && kfmi::attention_uses_pp(Hq, Hkv, S, D) && S % 8 == 0;
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
   r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;

@@ -54,5 +54,8 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
 // vt[b,h,d,s] = v[b,h,s,d] for the B*H heads of S rows of D.
 hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64_t S, int64_t D, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
+// Whether launch_attention runs the ping-pong kernel (the one that reads V^T)
+// for this shape (modes other than 'full').
+bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D);
 
 }  // namespace kfmi

@@ -373,9 +373,14 @@ def _optimized_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g
     return out
 
 
+PP_MIN_QBLOCKS = 24  # the library runs its ping-pong kernel from 24 query blocks of 128 rows
+
+
 def uses_vt(hq: int, hkv: int, s: int, d: int) -> bool:
-    """Whether launch_attention makes use of a ``vt`` scratch for this shape."""
-    return d == 128 and (hq // hkv) % 2 == 0 and s % 8 == 0
+    """Whether launch_attention makes use of a ``vt`` scratch for this shape
+    (the library's ping-pong kernel: D=128, even GQA ratio, S > 2944, and
+    16-byte aligned V^T rows)."""
+    return d == 128 and (hq // hkv) % 2 == 0 and -(-s // 128) >= PP_MIN_QBLOCKS and s % 8 == 0
 
 
 @_optimized_attention_op.register_fake
