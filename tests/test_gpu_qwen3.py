@@ -1,0 +1,41 @@
+"""Model-level caller (src/e2_qwen3_rope_prefill.py:129-169 in the reference):
+a randomly initialised Qwen3 model with Qwen3-8B's attention geometry, every
+attention layer switched to the fused op, stays as close to the HF
+norm/RoPE path with FP32 attention as a plain BF16-P attention does (the
+noise floor; random weights put the checkpoint-calibrated logit gates below
+it), keeps the NLL within 2.5e-2, and both arms replay as HIP graphs."""
+import pytest
+
+from helpers import announce
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def model(gpu):
+    from kernelfuser_amd.qwen3 import random_qwen3
+    return random_qwen3(layers=2, vocab=32000, seed=1701, device=gpu)
+
+
+@pytest.mark.parametrize("b,s", [(1, 128), (2, 300)])
+def test_qwen3_prefill_gates(model, b, s):
+    from kernelfuser_amd.qwen3 import run_row
+    announce(f"qwen3 random 2-layer prefill B={b} S={s}")
+    row = run_row(model, b, s, warmup=2, repeats=3, rounds=1, timing=(b == 1))
+    # random weights: the candidate must be as close to the FP32-attention
+    # reference as a plain BF16-P attention is (see noise_floor_gate)
+    assert row["status"] in ("pass", "pass_noise_floor"), (row["correctness"], row["noise_floor"])
+    m = row["correctness"]
+    assert m["pass_noise_floor"] and m["nll_abs_diff"] <= 2.5e-2 and m["relative_l2"] <= 2.5e-2
+    if b == 1:
+        assert row["timing"]["candidate_median_ms"] > 0
+
+
+def test_patch_restore(model):
+    from kernelfuser_amd.qwen3 import patch, restore
+    before = [m.forward for m in model.modules() if type(m).__name__ == "Qwen3Attention"]
+    saved = patch(model, "fused")
+    assert len(saved) == 2
+    restore(saved)
+    after = [m.forward for m in model.modules() if type(m).__name__ == "Qwen3Attention"]
+    assert before == after
