@@ -119,9 +119,8 @@ def headline(args, torch, kf):
     xs = xs_cpu.to("cuda:0")
     out = torch.empty_like(xs.q)
     kn = torch.empty_like(xs.k)
-    vt = torch.empty_like(xs.v)  # V^T scratch: the preparation launch writes it
     step = lambda: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn,
-                                       norm_style=args.norm_style, vt=vt)
+                                       norm_style=args.norm_style)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -140,16 +139,15 @@ def headline(args, torch, kf):
            "tflops": flops / (ms_step * 1e-3) / 1e12}
     # The two kernels separately (events on the launch stream).
     attn_ms = time_graph(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
-                                                           causal=True, fuse_q=True, norm_style=args.norm_style,
-                                                           vt=vt),
+                                                           causal=True, fuse_q=True, norm_style=args.norm_style),
                          20)
-    # The preparation launch of the step: K norm+RoPE rows plus V^T.
+    # The preparation launch of the step: K norm+RoPE rows.
     prep_ms = time_graph(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
-                                                        norm_style=args.norm_style, vt=vt), 100)
+                                                        norm_style=args.norm_style), 100)
     res["attention_kernel_us"] = attn_ms * 1e3
     res["prep_kernel_us"] = prep_ms * 1e3
     res["attention_kernel_tflops"] = flops / (attn_ms * 1e-3) / 1e12
-    prep_bytes = kf.k_prep_bytes(b, hkv, s, d) + 2 * xs.v.numel() * 2
+    prep_bytes = kf.k_prep_bytes(b, hkv, s, d)
     res["prep_bytes"] = prep_bytes
     res["prep_gbs"] = prep_bytes / (prep_ms * 1e-3) / 1e9
     return res, xs_cpu, out
@@ -189,13 +187,13 @@ def prefill_shapes(args, torch, kf):
     rows = []
     for b, s in [(1, 2048), (1, 8192), (4, 1000)]:
         xs = kf.make_inputs(b, s, QWEN3_8B, 2909).to("cuda:0")
-        out, kn, vt = torch.empty_like(xs.q), torch.empty_like(xs.k), torch.empty_like(xs.v)
+        out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
         ms = time_graph(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
-                                                       bn=64, kn=kn, norm_style=args.norm_style, vt=vt), 20)
+                                                       bn=64, kn=kn, norm_style=args.norm_style), 20)
         f = kf.attention_flops(b, hq, s, d, True)
         rows.append({"B": b, "S": s, "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
                      "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS})
-        del xs, out, kn, vt
+        del xs, out, kn
     return rows
 
 
@@ -268,10 +266,9 @@ def pmc_run(torch, kf):
     """A few launches of each kernel at the headline shapes plus one copy of
     known size, for rocprofv3 --pmc passes (FETCH_SIZE / WRITE_SIZE)."""
     xs = kf.make_inputs(1, 4096, QWEN3_8B, 1909).to("cuda:0")
-    out, kn, vt = torch.empty_like(xs.q), torch.empty_like(xs.k), torch.empty_like(xs.v)
+    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
     for _ in range(3):
-        kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn, norm_style="fp32",
-                            vt=vt)
+        kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn, norm_style="fp32")
     nr = kf.make_inputs(1, 8192, QWEN3_8B, 1909, with_v=False).to("cuda:0")
     qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
     for _ in range(3):
@@ -329,7 +326,7 @@ def main():
                      "kernel_us": head["attention_kernel_us"], "traffic": traffic},
         "kernels": {"attention_us": head["attention_kernel_us"],
                     "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
-                    "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows and V^T in one launch",
+                    "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows (one launch)",
                     "device_ms_per_step": head["device_ms_per_step"]},
     }
     if not args.quick:

@@ -104,9 +104,13 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
     issues them.
 
     ``vt`` (optional, shaped like V): scratch for V transposed per head.  When
-    given (and D=128, an even GQA ratio and S % 8 == 0), the preparation launch
-    also writes it and the attention kernel reads V^T rows, which halves its
-    LDS reads of V; results are identical.
+    given and the shape runs the ping-pong kernel (``uses_vt``), the
+    preparation launch also writes it and the attention kernel reads V^T rows
+    (one 16-byte LDS read per V operand instead of two transposing reads);
+    results are the same.  End to end it is slower on MI355X (the extra 2x V
+    bytes of the preparation launch cost more than the LDS reads save: S=4096
+    step 148.5 vs 144.0 us), so the allocating APIs do not use it; it serves
+    callers that already keep V transposed.
     """
     if mode not in ("full", "query", "unfused"):
         raise ValueError("Invalid fusion mode")
@@ -275,12 +279,10 @@ def fused(q, k, v, gq, gk, cos, sin, causal, eps=EPS, scale=None, norm_style="qw
     if tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d):
         raise ValueError("Expected rotary tables of S rows")
     out, kn = torch.empty_like(q), torch.empty_like(k)
-    vt = torch.empty_like(v) if uses_vt(h, k.shape[1], s, d) else None
     with torch.cuda.device(q.device):
-        prepare_attention((q, k, v, gq, gk, cos, sin), None, kn, only_k=True, rope=True, norm_style="hf", vt=vt,
-                          eps=eps)
+        prepare_attention((q, k, v, gq, gk, cos, sin), None, kn, only_k=True, rope=True, norm_style="hf", eps=eps)
         attention_prefill(q, kn, v, out, gq=gq, cos=cos, sin=sin, causal=causal, fuse_q=True, norm_style="hf",
-                          scale=scale, vt=vt, eps=eps)
+                          scale=scale, eps=eps)
     return out
 
 
@@ -364,12 +366,11 @@ def _optimized_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g
     out = torch.empty_like(q)
     kn = torch.empty_like(k)
     qn = torch.empty_like(q) if mode == "unfused" else None
-    vt = torch.empty_like(v) if uses_vt(q.shape[1], k.shape[1], q.shape[2], q.shape[3]) else None
     rotary = cos is not None
     xs = (q, k, v, gq, gk, cos if rotary else q, sin if rotary else k)
     with torch.cuda.device(q.device):
         launch_attention(xs, out, causal=causal, mode=mode, bm=128, bn=bn, rope=rotary, qn=qn, kn=kn,
-                         norm_style=norm_style, vt=vt)
+                         norm_style=norm_style)
     return out
 
 
