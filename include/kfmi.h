@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 4
+#define KFMI_ABI_VERSION 5
 
 /* status codes */
 #define KFMI_OK 0
@@ -90,7 +90,21 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
                         const void *cos, const void *sin, void *out,
                         int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                         double scale, float eps, int causal, int fuse_q, int norm_style,
-                        int bm, int bn, void *stream);
+                        int bm, int bn, void *work, int64_t work_bytes, void *stream);
+
+/* Bytes of the optional split-KV workspace `work` of the attention entry
+ * points for this shape (0: the shape never splits; -1: invalid shape).
+ * For causal D = 256 shapes with no more query blocks than the GPU has CUs
+ * (that kernel runs one workgroup per CU), the key range of the longest
+ * query blocks is split over two workgroups whose partial results are merged
+ * by the one finishing second; the workspace holds those partials and one
+ * counter per split block.  The
+ * caller zero-fills it once when allocating; each launch leaves the counters
+ * at zero again.  Calls that share a workspace must not overlap in time.
+ * With work == NULL or work_bytes below this size the launch does not split
+ * (same results, slower on those shapes).  No counterpart in the reference,
+ * whose launches never split a query block. */
+int64_t kfmi_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int causal);
 
 /* The launches of launch_attention (rope:661-677): mode QUERY prepares K
  * into kn (K rows only) then runs attention with the fused Q prologue; mode
@@ -112,7 +126,8 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
                                const void *sin, void *out, void *qn, void *kn, void *vt,
                                int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                                double scale, float eps, int causal, int mode,
-                               int norm_style, int bm, int bn, void *stream);
+                               int norm_style, int bm, int bn, void *work, int64_t work_bytes,
+                               void *stream);
 
 /* vt[b,h,d,s] = v[b,h,s,d] for B*H heads of S rows of D (D 128 or 256,
  * S % 8 == 0): the V^T scratch of kfmi_launch_attention_bf16, as a separate

@@ -20,6 +20,7 @@ from .ops import (  # noqa: F401
     model_scale,
     separate,
     attention_flops,
+    attention_workspace_bytes,
     attention_prefill,
     factored_attention,
     factored_qk_attention,
@@ -40,6 +41,6 @@ __all__ = [
     "EPS", "MODELS", "MODEL_QUERY_PRE_ATTN_SCALAR", "model_scale", "fused", "anchor", "separate",
     "optimized_attention", "attention_prefill", "launch_attention", "prepare_attention",
     "launch_factored_attention", "prepare_factored", "factored_attention", "factored_qk_attention",
-    "norm_rope", "uses_vt", "transpose_v", "attention_flops", "norm_rope_bytes", "k_prep_bytes", "make_inputs", "rope_tables",
+    "norm_rope", "uses_vt", "attention_workspace_bytes", "transpose_v", "attention_flops", "norm_rope_bytes", "k_prep_bytes", "make_inputs", "rope_tables",
     "Inputs", "QWEN3_8B", "GEMMA3_12B",
 ]

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -31,10 +31,10 @@ _D = ctypes.c_double
 SIGNATURES = {
     "kfmi_prepare_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _P],
     "kfmi_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D, _F, _I, _I, _I, _I, _I,
-                            _P],
+                            _P, _I64, _P],
     "kfmi_transpose_v_bf16": [_P, _P, _I64, _I64, _I64, _P],
     "kfmi_launch_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D,
-                                   _F, _I, _I, _I, _I, _I, _P],
+                                   _F, _I, _I, _I, _I, _I, _P, _I64, _P],
     "kfmi_factored_prepare_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "kfmi_factored_attention_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P],
     "kfmi_launch_factored_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I,
@@ -66,6 +66,8 @@ def load() -> ctypes.CDLL:
         lib.kfmi_abi_version.argtypes = []
         lib.kfmi_last_error.restype = ctypes.c_char_p
         lib.kfmi_last_error.argtypes = []
+        lib.kfmi_attention_workspace_bytes.restype = ctypes.c_int64
+        lib.kfmi_attention_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes

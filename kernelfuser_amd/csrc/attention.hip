@@ -79,7 +79,18 @@ struct AttnParams {
   int B, Hq, Hkv, n_qblocks, xcd_remap;
   float c_scale;  // scale*log2(e); for the factored prologues D^-1/2*log2(e)
   float eps;
+  // Split-KV plan of the general kernel (n_items > 0): work item r of the
+  // longest-first list covers query block it_qb[r] and key tiles
+  // [it_t0[r], it_t1[r]); it_sid[r] >= 0 marks one half of split block
+  // it_sid[r], whose partial results meet in `partials` and are merged by the
+  // half that finishes second (decided by `counters`, which end each launch
+  // at zero again).
+  int n_items;
+  int16_t it_qb[128], it_t0[128], it_t1[128], it_sid[128];
+  int *counters;
+  float *partials;
 };
+constexpr int MAX_SPLIT_ITEMS = 128;
 
 template <int ST>
 __device__ __forceinline__ float norm_elem(float x, float inv, float g) {
@@ -229,6 +240,23 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
     for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
     cl = (qvalid ? p.inv[qoff + qrow] : 1.0f) * p.c_scale;  // qk:621
   } else {
+    // gamma and the table rows are issued with the Q loads, so the prologue
+    // waits for one round trip to memory, not two
+    constexpr bool TAB = PRO == PRO_NORM_ROPE;
+    constexpr bool GAM = PRO == PRO_NORM || PRO == PRO_NORM_ROPE;
+    u32x4_t graw[GAM ? NC : 1], craw[TAB ? NC : 1], sraw[TAB ? NC : 1];
+    if constexpr (GAM) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) graw[c] = ld16(p.gq + 16 * c + 8 * g);
+    }
+    if constexpr (TAB) {
+      const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        craw[c] = ld16(p.cos + trow + 16 * c + 8 * g);
+        sraw[c] = ld16(p.sin + trow + 16 * c + 8 * g);
+      }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -252,8 +280,8 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
         float x1[8], x2[8], g1[8], g2[8], n1[8], n2[8], y1[8], y2[8];
         unpack8(raw[c], x1);
         unpack8(raw[c2], x2);
-        unpack8(ld16(p.gq + 16 * c + 8 * g), g1);
-        unpack8(ld16(p.gq + 16 * c2 + 8 * g), g2);
+        unpack8(graw[c], g1);
+        unpack8(graw[c2], g2);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           n1[j] = norm_elem<ST>(x1[j], inv, g1[j]);
@@ -261,11 +289,10 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
         }
         if constexpr (PRO == PRO_NORM_ROPE) {
           float cs1[8], sn1[8], cs2[8], sn2[8];
-          const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
-          unpack8(ld16(p.cos + trow + 16 * c + 8 * g), cs1);
-          unpack8(ld16(p.sin + trow + 16 * c + 8 * g), sn1);
-          unpack8(ld16(p.cos + trow + 16 * c2 + 8 * g), cs2);
-          unpack8(ld16(p.sin + trow + 16 * c2 + 8 * g), sn2);
+          unpack8(craw[c], cs1);
+          unpack8(sraw[c], sn1);
+          unpack8(craw[c2], cs2);
+          unpack8(sraw[c2], sn2);
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
             y1[j] = rope_elem<ST>(n1[j], n2[j], cs1[j], sn1[j], true);
@@ -820,12 +847,21 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   const int lr = lane & 31;  // query row of this lane within the wave
   const int64_t S = p.S;
 
-  // ---- work item: heaviest query blocks first; KV groups pinned to an XCD ----
+  // ---- work item: heaviest query blocks (or split halves) first; KV groups
+  // pinned to an XCD ----
   const int nbh = p.B * p.Hq;
   const int bid = blockIdx.x;
   const int rank = bid / nbh;
   const int r = bid - rank * nbh;
-  const int qb = CAUSAL ? p.n_qblocks - 1 - rank : rank;
+  int qb, t0 = 0, t1 = -1, sid = -1;
+  if (p.n_items > 0) {
+    qb = p.it_qb[rank];
+    t0 = p.it_t0[rank];
+    t1 = p.it_t1[rank];
+    sid = p.it_sid[rank];
+  } else {
+    qb = CAUSAL ? p.n_qblocks - 1 - rank : rank;
+  }
   const int G = p.Hq / p.Hkv;
   int b, h;
   if (p.xcd_remap) {
@@ -873,16 +909,17 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   const int qrow = q0 + lr;
   const bool qvalid = qrow < S;
 
-  // ---- KV tile counts ----
+  // ---- KV tile range [t0, nT) of this work item ----
   const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
-  const int nT = (int)((kv_end + BN - 1) / BN);
+  const int nT = t1 >= 0 ? t1 : (int)((kv_end + BN - 1) / BN);
   const int64_t wave_end = CAUSAL ? ((int64_t)q0 + 32 < S ? (int64_t)q0 + 32 : S) : S;
-  const int nTw = q0 < S ? (int)((wave_end + BN - 1) / BN) : 0;  // tiles with any unmasked key
+  const int nTw0 = q0 < S ? (int)((wave_end + BN - 1) / BN) : 0;  // tiles with any unmasked key
+  const int nTw = nTw0 < nT ? nTw0 : nT;
 
   // Start the first copies before the prologue's own global loads.
-  copy_k(0, K0);
-  copy_v(0, V0);
-  if (nT > 1) copy_k(1, K1);
+  copy_k(t0, K0);
+  copy_v(t0, V0);
+  if (t0 + 1 < nT) copy_k(t0 + 1, K1);
 
   bf16x8_t qreg[NC];
   float cl;
@@ -925,20 +962,83 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   f32x16_t sa[NKB], sb[NKB];
   wait_copies();
   __syncthreads();
-  if (nTw > 0) {
+  if (t0 < nTw) {
     if constexpr (FK)
-      gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, K0, kra, qreg, sa, p, 0, g, lr);
+      gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, K0, kra, qreg, sa, p, t0 * BN, g, lr);
     else
       gemm1<D, BN>(smem, K0, kra, qreg, sa);
   }
-  for (int t = 0;;) {
+  for (int t = t0;;) {
     iteration(std::integral_constant<int, 0>{}, t, sa, sb);
     if (++t >= nT) break;
     iteration(std::integral_constant<int, 1>{}, t, sb, sa);
     if (++t >= nT) break;
   }
 
-  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+  // the host plans splits for D = 256 only (plan_split)
+  if (D != 256 || sid < 0) {
+    store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+    return;
+  }
+  // ---- one half of a split query block: publish the partial state (O
+  // relative to m_run, the lane's row-sum share, m_run); the half that
+  // finishes second reads the other's, merges and stores, and re-arms the
+  // counter.  Slot layout (floats): O quad q of thread tid at
+  // [(q * 256 + tid) * 4], m_run at [NQ * 1024 + tid], l_run after it.
+  //
+  // The slots are written and read with agent-coherent accesses (cache
+  // policy SC1, what the compiler gives agent-scope atomic accesses on
+  // gfx950): a store that has completed (vmcnt) is visible to SC1 loads on
+  // any XCD.  That orders the handover through the counter without the L2
+  // writeback and invalidate that a device-scope fence costs.
+  constexpr int NQ = NDB * 4;
+  constexpr int SLOT = (NQ * 4 + 2) * 256;  // floats
+  constexpr int SC1 = 16;
+  const int part = t0 > 0 ? 1 : 0;
+  // wave-uniform (sid, b, h are per workgroup): keeps the descriptors in SGPRs
+  const int pair = __builtin_amdgcn_readfirstlane(sid * nbh + (b * p.Hq + h));
+  const auto mine =
+      __builtin_amdgcn_make_buffer_rsrc(p.partials + (int64_t)(2 * pair + part) * SLOT, 0, SLOT * 4, 0x00020000);
+  const auto other =
+      __builtin_amdgcn_make_buffer_rsrc(p.partials + (int64_t)(2 * pair + 1 - part) * SLOT, 0, SLOT * 4, 0x00020000);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const f32x4_t v = {o[q / 4][(q % 4) * 4], o[q / 4][(q % 4) * 4 + 1], o[q / 4][(q % 4) * 4 + 2],
+                       o[q / 4][(q % 4) * 4 + 3]};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), mine, (q * 256 + tid) * 16, 0, SC1);
+  }
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sm.m_run), mine, (NQ * 1024 + tid) * 4, 0, SC1);
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sm.l_run), mine, (NQ * 1024 + 256 + tid) * 4, 0,
+                                        SC1);
+  wait_copies();  // every store of this thread has completed
+  __syncthreads();
+  __shared__ int arrived_before;
+  if (tid == 0) arrived_before = atomicAdd(p.counters + pair, 1);
+  __syncthreads();
+  if (arrived_before == 0) return;  // the other half merges
+  // Merge in fixed (first half, second half) operand order, whichever half
+  // runs it, with explicit fmaf, so the result does not depend on timing.
+  const float mo = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(other, (NQ * 1024 + tid) * 4, 0, SC1));
+  const float lo =
+      __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(other, (NQ * 1024 + 256 + tid) * 4, 0, SC1));
+  const float m0 = part == 0 ? sm.m_run : mo, m1 = part == 0 ? mo : sm.m_run;
+  const float m = fmaxf(m0, m1);
+  // rows past S may hold -inf maxima in both halves; they are not stored
+  const float a0 = m0 == m ? 1.0f : __builtin_amdgcn_exp2f(m0 - m);
+  const float a1 = m1 == m ? 1.0f : __builtin_amdgcn_exp2f(m1 - m);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const f32x4_t v = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(other, (q * 256 + tid) * 16, 0, SC1));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float r = o[q / 4][(q % 4) * 4 + k];
+      const float x0 = part == 0 ? r : v[k], x1 = part == 0 ? v[k] : r;
+      o[q / 4][(q % 4) * 4 + k] = fmaf(x0, a0, x1 * a1);
+    }
+  }
+  const float l0 = part == 0 ? sm.l_run : lo, l1 = part == 0 ? lo : sm.l_run;
+  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, fmaf(l0, a0, l1 * a1), o);
+  if (tid == 0) atomicExch(p.counters + pair, 0);
 }
 
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
@@ -992,9 +1092,93 @@ bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D) {
   return D == 128 && (Hq / Hkv) % 2 == 0 && (S + 127) / 128 >= PP_MIN_QBLOCKS;
 }
 
+namespace {
+
+// Compute units of the current device (256 on MI355X), cached per device;
+// 256 when no device can be queried.  Scheduling only: results never depend
+// on it.
+int64_t device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cached[dev];
+}
+
+// Split-KV plan for the general kernel at D = 256, which runs one workgroup
+// per CU: with no more work items than CUs, longest-first ordering cannot
+// balance a causal grid (the heaviest query block alone sets the time, and
+// no co-resident workgroup fills the gap).  Blocks with more key tiles than
+// half the maximum are then split into two halves of their key range (the
+// second holds the diagonal), and all items are listed longest first.  At
+// D = 128 two workgroups share each CU and one already keeps it nearly
+// busy, so the extra prologues of a split cost more than the balance gains.
+
+struct SplitPlan {
+  int n_items = 0, n_split = 0;
+  int16_t qb[MAX_SPLIT_ITEMS], t0[MAX_SPLIT_ITEMS], t1[MAX_SPLIT_ITEMS], sid[MAX_SPLIT_ITEMS];
+};
+
+bool plan_split(int64_t B, int64_t Hq, int64_t S, int64_t D, bool causal, int64_t cus, SplitPlan &pl) {
+  const int64_t BM = 128, BN = D == 128 ? 64 : 32;
+  const int64_t nqb = (S + BM - 1) / BM;
+  if (D != 256 || !causal || nqb < 2 || B * Hq * nqb > cus) return false;
+  auto tiles = [&](int64_t qb) { return ((qb + 1) * BM < S ? (qb + 1) * BM : S) + BN - 1; };
+  const int64_t t_max = tiles(nqb - 1) / BN;
+  const int64_t half = (t_max + 1) / 2;
+  struct Item { int qb, t0, t1, sid; };
+  Item items[MAX_SPLIT_ITEMS];
+  int n = 0, n_split = 0;
+  for (int64_t qb = 0; qb < nqb; ++qb) {
+    const int nt = (int)(tiles(qb) / BN);
+    if (nt > half) {
+      if (n + 2 > MAX_SPLIT_ITEMS) return false;
+      const int mid = (nt + 1) / 2;
+      items[n++] = {(int)qb, 0, mid, n_split};
+      items[n++] = {(int)qb, mid, nt, n_split};
+      ++n_split;
+    } else {
+      if (n + 1 > MAX_SPLIT_ITEMS) return false;
+      items[n++] = {(int)qb, 0, nt, -1};
+    }
+  }
+  if (n_split == 0) return false;
+  // longest first (insertion sort: n <= 128)
+  for (int i = 1; i < n; ++i)
+    for (int j = i; j > 0 && items[j].t1 - items[j].t0 > items[j - 1].t1 - items[j - 1].t0; --j) {
+      const Item t = items[j]; items[j] = items[j - 1]; items[j - 1] = t;
+    }
+  pl.n_items = n;
+  pl.n_split = n_split;
+  for (int i = 0; i < n; ++i) {
+    pl.qb[i] = (int16_t)items[i].qb; pl.t0[i] = (int16_t)items[i].t0;
+    pl.t1[i] = (int16_t)items[i].t1; pl.sid[i] = (int16_t)items[i].sid;
+  }
+  return true;
+}
+
+int64_t split_counter_bytes(int64_t pairs) { return (pairs * 4 + 255) / 256 * 256; }
+int64_t split_partial_bytes(int64_t pairs, int64_t D) { return pairs * 2 * (D / 2 + 2) * 256 * 4; }
+
+}  // namespace
+
+int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal) {
+  if (attention_uses_pp(Hq, Hkv, S, D)) return 0;
+  SplitPlan pl;
+  if (!plan_split(B, Hq, S, D, causal, device_cus(), pl)) return 0;
+  const int64_t pairs = (int64_t)pl.n_split * B * Hq;
+  return split_counter_bytes(pairs) + split_partial_bytes(pairs, D);
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   constexpr double LOG2E = 1.4426950408889634;
   AttnParams p;
+  p.n_items = 0;
+  p.counters = nullptr;
+  p.partials = nullptr;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
   p.gk = a.gk;
   p.out = a.out; p.inv = a.inv;
@@ -1019,6 +1203,19 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     const int nbh = p.B * p.Hq;
     p.xcd_remap = (nbh % 8 == 0 && (p.B * p.Hkv) % 8 == 0) ? 1 : 0;
     blocks = p.n_qblocks * nbh;
+    SplitPlan pl;
+    if (a.work && plan_split(a.B, a.Hq, a.S, a.D, a.causal, device_cus(), pl)) {
+      const int64_t pairs = (int64_t)pl.n_split * nbh;
+      if (a.work_bytes >= split_counter_bytes(pairs) + split_partial_bytes(pairs, a.D)) {
+        p.n_items = pl.n_items;
+        for (int i = 0; i < pl.n_items; ++i) {
+          p.it_qb[i] = pl.qb[i]; p.it_t0[i] = pl.t0[i]; p.it_t1[i] = pl.t1[i]; p.it_sid[i] = pl.sid[i];
+        }
+        p.counters = (int *)a.work;
+        p.partials = (float *)((char *)a.work + split_counter_bytes(pairs));
+        blocks = pl.n_items * nbh;
+      }
+    }
   }
   if (a.D == 128) {
     return a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, pp, blocks, stream)

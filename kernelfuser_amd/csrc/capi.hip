@@ -130,7 +130,8 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *g
 static int attention_impl(const void *q, const void *k, const void *v, const void *vt, const void *gq,
                           const void *gk, const void *cos, const void *sin, void *out, float *inv, int64_t B, int64_t Hq,
                           int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal, int prologue,
-                          int style, int bm, int bn, hipStream_t stream) {
+                          int style, int bm, int bn, hipStream_t stream, void *work = nullptr,
+                          int64_t work_bytes = 0) {
   kfmi::AttnArgs a{};
   a.q = (const uint16_t *)q; a.k = (const uint16_t *)k; a.v = (const uint16_t *)v; a.gq = (const uint16_t *)gq;
   a.vt = (const uint16_t *)vt;
@@ -139,13 +140,26 @@ static int attention_impl(const void *q, const void *k, const void *v, const voi
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
   a.causal = causal != 0; a.prologue = prologue; a.style = style; a.scale = scale; a.eps = eps;
   a.bm = bm; a.bn = bn;
+  a.work = work; a.work_bytes = work_bytes;
   return launch_status(kfmi::launch_attention(a, stream), "attention launch");
+}
+
+int64_t kfmi_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int causal) {
+  if (check_shape(B, Hq, Hkv, S, D) != KFMI_OK) return -1;
+  g_error.clear();
+  return kfmi::attention_workspace_bytes(B, Hq, Hkv, S, D, causal != 0);
+}
+
+static int check_work(const void *work, int64_t work_bytes) {
+  if (work_bytes < 0) return fail(KFMI_EINVAL, "work_bytes must be >= 0");
+  if (work && !aligned16(work)) return fail(KFMI_EINVAL, "work must be 16-byte aligned");
+  return KFMI_OK;
 }
 
 int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void *vt, const void *gq, const void *cos,
                         const void *sin, void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
                         double scale, float eps, int causal, int fuse_q, int norm_style, int bm, int bn,
-                        void *stream) {
+                        void *work, int64_t work_bytes, void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
   KFMI_TRY(check_tiles(bm, bn));
@@ -154,23 +168,26 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
   if (fuse_q) KFMI_TRY(check_ptrs({{gq, "gq"}}));
   if (fuse_q && cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
+  KFMI_TRY(check_work(work, work_bytes));
   KFMI_TRY(check_device());
   const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
   return attention_impl(q, k, v, vt, gq, nullptr, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal, pro,
-                        style_of(norm_style), bm, bn, (hipStream_t)stream);
+                        style_of(norm_style), bm, bn, (hipStream_t)stream, work, work_bytes);
 }
 
 int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
                                const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt, int64_t B,
                                int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal,
-                               int mode, int norm_style, int bm, int bn, void *stream) {
+                               int mode, int norm_style, int bm, int bn, void *work, int64_t work_bytes,
+                               void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
   KFMI_TRY(check_tiles(bm, bn));
   if (mode != KFMI_MODE_QUERY && mode != KFMI_MODE_UNFUSED && mode != KFMI_MODE_FULL)
     return fail(KFMI_EINVAL, "Invalid fusion mode %d", mode);
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}}));
+  KFMI_TRY(check_work(work, work_bytes));
   if (mode == KFMI_MODE_FULL) {  // one launch, K normalised per tile; no scratch (rope:671-677)
     if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
     if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
@@ -178,7 +195,7 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
     KFMI_TRY(check_device());
     return attention_impl(q, k, v, nullptr, gq, gk, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal,
                           cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM, style_of(norm_style), bm, bn,
-                          (hipStream_t)stream);
+                          (hipStream_t)stream, work, work_bytes);
   }
   if (kn == nullptr || (mode == KFMI_MODE_UNFUSED && qn == nullptr)) return fail(KFMI_EINVAL, "Missing scratch buffers");
   KFMI_TRY(check_ptrs({{kn, "kn"}}));
@@ -205,7 +222,7 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
   const bool query = mode == KFMI_MODE_QUERY;
   const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, nullptr, cos, sin, out, nullptr, B, Hq, Hkv, S, D,
-                        scale, eps, causal, pro, style_of(norm_style), bm, bn, (hipStream_t)stream);
+                        scale, eps, causal, pro, style_of(norm_style), bm, bn, (hipStream_t)stream, work, work_bytes);
 }
 
 int kfmi_transpose_v_bf16(const void *v, void *vt, int64_t BH, int64_t S, int64_t D, void *stream) {

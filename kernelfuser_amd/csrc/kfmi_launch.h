@@ -47,6 +47,8 @@ struct AttnArgs {
   double scale;  // multiplies q.k (ignored by the factored prologues: D^-1/2)
   float eps;
   int bm, bn;
+  void *work;          // split-KV workspace (counters + partial results) or NULL
+  int64_t work_bytes;  // its size; too small = no split
 };
 
 // Both return hipSuccess or the launch error.  Arguments are validated by the caller.
@@ -57,5 +59,8 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
 // Whether launch_attention runs the ping-pong kernel (the one that reads V^T)
 // for this shape (modes other than 'full').
 bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D);
+// Workspace bytes with which launch_attention splits the key range of the
+// longest causal query blocks over two workgroups (0: this shape never splits).
+int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal);
 
 }  // namespace kfmi

@@ -66,6 +66,52 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 
 
 # ---------------------------------------------------------------------------
+# Split-KV workspace (see kfmi_attention_workspace_bytes): one zero-filled
+# buffer per device, grown on demand outside graph capture; each launch leaves
+# its counters at zero again.  Launches on one device share it, so they must
+# run in stream order (as torch's current stream does).
+# ---------------------------------------------------------------------------
+
+_work_cache: dict[int, torch.Tensor] = {}
+
+
+def attention_workspace_bytes(b: int, hq: int, hkv: int, s: int, d: int, causal: bool) -> int:
+    """Workspace bytes with which attention splits the longest causal query
+    blocks over two workgroups for this shape (0: it never splits)."""
+    n = int(_lib.load().kfmi_attention_workspace_bytes(b, hq, hkv, s, d, int(bool(causal))))
+    if n < 0:
+        raise ValueError("invalid attention shape")
+    return n
+
+
+def _workspace(device: torch.device, nbytes: int):
+    """The device's cached workspace of at least nbytes, or None (no split)
+    when it would have to be allocated during graph capture."""
+    if nbytes <= 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _work_cache.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        buf = torch.zeros(max(nbytes, 0 if buf is None else 2 * buf.numel()), dtype=torch.uint8, device=device)
+        torch.cuda.current_stream(device).synchronize()
+        _work_cache[idx] = buf
+    return buf
+
+
+def _work_args(work, q, hkv, causal):
+    """(pointer, bytes) of the split workspace: ``work=None`` uses the cached
+    one when the shape splits; a tensor is used as given."""
+    if work is None:
+        b, h, s, d = q.shape
+        work = _workspace(q.device, attention_workspace_bytes(b, h, hkv, s, d, causal))
+    if work is None:
+        return None, 0
+    return work.data_ptr(), work.numel() * work.element_size()
+
+
+# ---------------------------------------------------------------------------
 # Low-level launchers (caller-preallocated buffers, no checks beyond the C ABI's)
 # ---------------------------------------------------------------------------
 
@@ -92,7 +138,7 @@ def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_nor
 
 
 def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, warps=4, stages=1,
-                     gather=True, rope=True, hf_norm=True, qn=None, kn=None, norm_style=None, vt=None):
+                     gather=True, rope=True, hf_norm=True, qn=None, kn=None, norm_style=None, vt=None, work=None):
     """Preparation + attention launches of the reference launcher (rope:661-677).
 
     ``mode='query'``: K is prepared once into ``kn``; Q's norm (+RoPE) runs in the
@@ -111,6 +157,9 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
     bytes of the preparation launch cost more than the LDS reads save: S=4096
     step 148.5 vs 144.0 us), so the allocating APIs do not use it; it serves
     callers that already keep V transposed.
+
+    ``work``: split-KV workspace (a zero-filled tensor of at least
+    ``attention_workspace_bytes`` bytes); ``None`` uses a cached one per device.
     """
     if mode not in ("full", "query", "unfused"):
         raise ValueError("Invalid fusion mode")
@@ -118,17 +167,18 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
         raise ValueError("Missing scratch buffers")
     q, k, v, gq, gk, cos, sin = inputs
     b, h, s, d = q.shape
+    wp, wb = _work_args(work, q, k.shape[1], causal)
     _lib.call("kfmi_launch_attention_bf16",
               ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk),
               ptr(cos) if rope else None, ptr(sin) if rope else None,
               ptr(out), ptr(qn), ptr(kn), ptr(vt),
               b, h, k.shape[1], s, d, float(d) ** -0.5, EPS, int(bool(causal)),
               {"query": MODE_QUERY, "unfused": MODE_UNFUSED, "full": MODE_FULL}[mode], _style(norm_style, hf_norm),
-              _bm(bm), _bn(bn), stream_of(q))
+              _bm(bm), _bn(bn), wp, wb, stream_of(q))
 
 
 def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=False, fuse_q=True,
-                      norm_style="fp32", bm=128, bn=64, scale=None, vt=None, eps=EPS):
+                      norm_style="fp32", bm=128, bn=64, scale=None, vt=None, eps=EPS, work=None):
     """The attention launch alone (attention_v2_kernel, rope:608-649) on a prepared
     ``kn``.  ``fuse_q=True``: raw ``q`` with its RMSNorm (``gq``) and, when both
     tables are given, RoPE in the prologue (FUSE_Q); ``fuse_q=False``: ``q`` is
@@ -136,9 +186,10 @@ def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=Fals
     transposed per head (see ``transpose_v``), read instead of ``v`` when the
     shape allows it (``uses_vt``)."""
     b, h, s, d = q.shape
+    wp, wb = _work_args(work, q, kn.shape[1], causal)
     _lib.call("kfmi_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(vt), ptr(gq), ptr(cos), ptr(sin), ptr(out),
               b, h, kn.shape[1], s, d, float(d) ** -0.5 if scale is None else float(scale), float(eps),
-              int(bool(causal)), int(bool(fuse_q)), NORM_STYLES[norm_style], _bm(bm), _bn(bn), stream_of(q))
+              int(bool(causal)), int(bool(fuse_q)), NORM_STYLES[norm_style], _bm(bm), _bn(bn), wp, wb, stream_of(q))
 
 
 def transpose_v(v, vt):

@@ -26,8 +26,9 @@ def lib():
 
 def test_header_declares_the_bound_entry_points():
     names = _declared()
-    assert "kfmi_abi_version" in names and "kfmi_last_error" in names
-    assert set(_lib.SIGNATURES) == set(names) - {"kfmi_abi_version", "kfmi_last_error"}
+    queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes"}
+    assert queries <= set(names)
+    assert set(_lib.SIGNATURES) == set(names) - queries
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -60,26 +61,30 @@ CASES = [
     ("kfmi_prepare_bf16", (P, P, None, P, P, P, P, P, P, P, 1, 32, 8, 16, 128, 1e-6, 2, 2, None), "v must not"),
     ("kfmi_prepare_bf16", (P, P, P, P, P, P, P, P, P, P, 1, 32, 8, 12, 128, 1e-6, 2, 2, None), "S % 8"),
     ("kfmi_prepare_bf16", (P + 2, P, None, P, P, P, P, P, P, None, 1, 32, 8, 16, 128, 1e-6, 2, 0, None), "aligned"),
-    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 33, 64, None), "bm"),
-    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 48, None), "bn"),
-    ("kfmi_attention_bf16", (P, P, P, None, P, P, None, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 33, 64, None, 0, None), "bm"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 48, None, 0, None), "bn"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, None, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None, 0, None),
      "both rotary"),
-    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.0, 1e-6, 1, 1, 2, 128, 64, None),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.0, 1e-6, 1, 1, 2, 128, 64, None, 0, None),
      "scale"),
-    ("kfmi_attention_bf16", (P, P, P, None, None, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None),
+    ("kfmi_attention_bf16", (P, P, P, None, None, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None, 0, None),
      "gq"),
     ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 2 ** 16, 8, 2 ** 12, 256, 0.1, 1e-6, 1, 1, 2, 128, 64,
-                             None), "2^31"),
+                             None, 0, None), "2^31"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None, -1, None),
+     "work_bytes"),
+    ("kfmi_attention_bf16", (P, P, P, None, P, P, P, P, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, P + 4, 64, None),
+     "work must be"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 5, 2,
-                                    128, 64, None), "Invalid fusion mode"),
+                                    128, 64, None, 0, None), "Invalid fusion mode"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, None, P, P, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 2,
-                                    2, 128, 64, None), "gk must not"),
+                                    2, 128, 64, None, 0, None), "gk must not"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, None, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 2,
-                                    2, 128, 64, None), "both rotary"),
+                                    2, 128, 64, None, 0, None), "both rotary"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, None, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 0, 2,
-                                    128, 64, None), "Missing scratch buffers"),
+                                    128, 64, None, 0, None), "Missing scratch buffers"),
     ("kfmi_launch_attention_bf16", (P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1, 1e-6, 1, 1, 2,
-                                    128, 64, None), "Missing scratch buffers"),
+                                    128, 64, None, 0, None), "Missing scratch buffers"),
     ("kfmi_transpose_v_bf16", (P, P, 4, 100, 128, None), "multiple of 8"),
     ("kfmi_transpose_v_bf16", (P, P, 4, 64, 96, None), "D must be"),
     ("kfmi_transpose_v_bf16", (P, None, 4, 64, 128, None), "vt must not"),
@@ -101,10 +106,23 @@ def test_invalid_arguments_fail_before_launch(lib, name, args, fragment):
     assert fragment in _err(lib), _err(lib)
 
 
+def test_workspace_bytes_query(lib):
+    f = lib.kfmi_attention_workspace_bytes
+    assert f(1, 32, 8, 0, 128, 1) == -1  # invalid shape
+    assert f(1, 32, 8, 8192, 128, 1) == 0  # runs the ping-pong kernel: no split
+    assert f(1, 32, 8, 2048, 128, 1) == 0  # D = 128: two workgroups per CU, no split
+    assert f(1, 16, 8, 2048, 256, 0) == 0  # not causal: nothing to balance
+    assert f(4, 16, 8, 2048, 256, 1) == 0  # more work items than CUs
+    n = f(1, 16, 8, 2048, 256, 1)  # 256 items = 256 CUs: the long blocks split
+    # 8 split blocks x 16 heads: counters + 2 halves of 256 threads x (128 + 2) floats
+    pairs = 8 * 16
+    assert n == (pairs * 4 + 255) // 256 * 256 + pairs * 2 * 130 * 256 * 4
+
+
 def test_call_maps_einval_to_value_error(lib):
     with pytest.raises(ValueError, match="Invalid fusion mode"):
         _lib.call("kfmi_launch_attention_bf16", P, P, P, P, P, P, P, P, None, P, None, 1, 32, 8, 16, 128, 0.1,
-                  1e-6, 1, 9, 2, 128, 64, None)
+                  1e-6, 1, 9, 2, 128, 64, None, 0, None)
 
 
 def test_last_error_is_per_thread(lib):

@@ -1,0 +1,88 @@
+"""Split-KV execution of the general attention kernel at D = 256 (one
+workgroup per CU): for causal shapes whose work items would just fill the
+GPU, the longest query blocks' key ranges are split over two workgroups and
+merged by the one finishing second.
+
+Results are bit-identical from launch to launch (the merge runs in a fixed
+order whichever half performs it), within a few ulp of the unsplit launch
+(each half rounds its probabilities relative to its own running max), pass
+the oracle gate, and stay correct over repeated launches and graph replays
+(the merge counters re-arm themselves)."""
+import pytest
+import torch
+
+import oracle
+from helpers import announce, bf16_ulp
+from kernelfuser_amd import attention_prefill, attention_workspace_bytes, make_inputs, prepare_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(xs, kn, causal, work, style="fp32"):
+    out = torch.empty_like(xs.q)
+    attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin, causal=causal, norm_style=style,
+                      work=work)
+    return out
+
+
+@pytest.mark.parametrize("geom,b,s", [((16, 8, 256), 1, 2048), ((16, 8, 256), 1, 1900), ((8, 4, 256), 1, 2048),
+                                      ((4, 2, 256), 1, 1000)])
+def test_split_matches_unsplit(gpu, geom, b, s):
+    hq, hkv, d = geom
+    nbytes = attention_workspace_bytes(b, hq, hkv, s, d, True)
+    assert nbytes > 0, "shape expected to split"
+    xs = make_inputs(b, s, geom, 1212).to(gpu)
+    kn = torch.empty_like(xs.k)
+    prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+    work = torch.zeros(nbytes, dtype=torch.uint8, device=gpu)
+    announce(f"split {geom} B={b} S={s} ({nbytes} B workspace)")
+    ref_unsplit = _run(xs, kn, True, torch.empty(0, dtype=torch.uint8, device=gpu))
+    first = _run(xs, kn, True, work)
+    second = _run(xs, kn, True, work)  # counters must have re-armed
+    torch.cuda.synchronize()
+    pairs = nbytes // (2 * (d // 2 + 2) * 256 * 4)  # one counter per split (block, head) pair
+    counters = work[:4 * pairs].view(torch.int32)
+    assert int(counters.abs().sum()) == 0, counters.nonzero().flatten().tolist()[:8]  # re-armed
+    assert torch.equal(first, second), float((first.float() - second.float()).abs().max())
+    # each half rounds its probabilities to BF16 relative to its own running
+    # max, so split rows differ from unsplit ones by a few ulp (a wrong merge
+    # would be off by O(0.1))
+    d_ = (first.float() - ref_unsplit.float()).abs()
+    tol = 4 * bf16_ulp(torch.maximum(first.float().abs(), ref_unsplit.float().abs())) + 1e-3
+    assert bool((d_ <= tol).all()), float((d_ / tol).max())
+    rows = torch.unique(torch.cat([torch.arange(0, 3), torch.randint(0, s, (30,), generator=torch.Generator().manual_seed(s)),
+                                   torch.arange(s - 130, s)]))
+    ref = oracle.oracle_rows_fp32(*[t.cpu() for t in xs.astuple()], rows, True)
+    assert oracle.attention_gate(first[:, :, rows.to(gpu)].cpu(), ref)["pass"]
+
+
+def test_split_graph_replays(gpu):
+    xs = make_inputs(1, 2048, (16, 8, 256), 1313).to(gpu)
+    kn = torch.empty_like(xs.k)
+    prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="hf")
+    work = torch.zeros(attention_workspace_bytes(1, 16, 8, 2048, 256, True), dtype=torch.uint8, device=gpu)
+    out = torch.empty_like(xs.q)
+    fn = lambda: attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin, causal=True,
+                                   norm_style="hf", work=work)
+    announce("split graph replays")
+    fn()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        fn()  # eager launches between replays share the workspace
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
