@@ -77,6 +77,9 @@ struct AttnParams {
   float *inv;
   int64_t S;
   int B, Hq, Hkv, n_qblocks, xcd_remap;
+  // ping-pong kernel, persistent mode: number of (long, short) query-block
+  // pairs; 0 = one item per workgroup
+  int pp_units;
   float c_scale;  // scale*log2(e); for the factored prologues D^-1/2*log2(e)
   float eps;
   // Split-KV plan of the general kernel (n_items > 0): work item r of the
@@ -660,24 +663,13 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   const int lr = lane & 31;
   const int64_t S = p.S;
 
-  // ---- work item: (query block, KV head, head pair); heaviest blocks first;
-  // all head pairs of a KV head on one XCD so its K/V stay in that L2 ----
   const int G = p.Hq / p.Hkv;
-  const int HP = G / 2;
+  const int HP = G / 2;  // head pairs per KV head
   const int npairs = p.B * p.Hkv * HP;
-  const int bid = blockIdx.x;
-  const int rank = bid / npairs;
-  const int r = bid - rank * npairs;
-  const int qb = CAUSAL ? p.n_qblocks - 1 - rank : rank;
-  int kvi, j;
-  if (p.xcd_remap) {
-    const int xcd = r & 7, jj = r >> 3;
-    kvi = xcd + 8 * (jj / HP);
-    j = jj % HP;
-  } else {
-    kvi = r / HP;
-    j = r - kvi * HP;
-  }
+  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
+
+  // One work item: query block qb of head pair j of KV head kvi.
+  auto run = [&](const int qb, const int kvi, const int j) {
   const int b = kvi / p.Hkv;
   const int kvh = kvi - b * p.Hkv;
   const int h = kvh * G + 2 * j + grp;
@@ -687,7 +679,6 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   const uint32_t head_bytes = (uint32_t)(S * 2 * D);
   const i32x4_t krs = buffer_rsrc(p.k + kvoff * D, head_bytes);
   const i32x4_t vrs = buffer_rsrc((VT ? p.vt : p.v) + kvoff * D, head_bytes);
-  const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
   uint32_t kvo[LPW], vvo[LPW];
 #pragma unroll
   for (int i = 0; i < LPW; ++i) {
@@ -820,6 +811,53 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   }
 
   store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+  };
+
+  // ---- work items.  Persistent (pp_units > 0, causal): workgroup bid takes
+  // units bid, bid + grid, ...; unit u pairs query blocks R-1-m and m of one
+  // head pair, so every unit holds the same number of key tiles, and the
+  // grid (a multiple of 8) keeps unit u on XCD u % 8, the home of its KV
+  // head.  Otherwise one item per workgroup, heaviest blocks first.  Both
+  // share one call site of `run`, so its body is emitted once. ----
+  const int R = p.n_qblocks;
+  int u = blockIdx.x, phase = 0;
+  for (;;) {
+    int qb, kvi, j;
+    if (p.pp_units > 0) {
+      if (u >= p.pp_units) break;
+      const int per_kv = HP * ((R + 1) / 2);
+      const int rest = u >> 3;
+      kvi = (u & 7) + 8 * (rest / per_kv);
+      const int rem = rest % per_kv;
+      j = rem % HP;
+      const int m = rem / HP;
+      qb = phase == 0 ? R - 1 - m : m;
+      if (phase == 0 && m != R - 1 - m) {
+        phase = 1;
+      } else {
+        phase = 0;
+        u += gridDim.x;
+      }
+    } else {
+      if (u < 0) break;
+      const int bid = u;
+      u = -1;
+      const int rank = bid / npairs;
+      const int r = bid - rank * npairs;
+      qb = CAUSAL ? R - 1 - rank : rank;
+      if (p.xcd_remap) {
+        // all head pairs of a KV head on one XCD so its K/V stay in that L2
+        const int xcd = r & 7, jj = r >> 3;
+        kvi = xcd + 8 * (jj / HP);
+        j = jj % HP;
+      } else {
+        kvi = r / HP;
+        j = r - kvi * HP;
+      }
+    }
+    run(qb, kvi, j);
+    __syncthreads();  // the next item refills the LDS buffers
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1177,6 +1215,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   constexpr double LOG2E = 1.4426950408889634;
   AttnParams p;
   p.n_items = 0;
+  p.pp_units = 0;
   p.counters = nullptr;
   p.partials = nullptr;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
@@ -1199,6 +1238,13 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     const int npairs = p.B * p.Hkv * (G / 2);
     p.xcd_remap = ((p.B * p.Hkv) % 8 == 0 && npairs % 8 == 0) ? 1 : 0;
     blocks = p.n_qblocks * npairs;
+    // persistent mode when the (long, short) pairs fill every CU equally
+    const int64_t cus = device_cus();
+    const int64_t units = (int64_t)npairs * ((p.n_qblocks + 1) / 2);
+    if (a.causal && p.xcd_remap && cus % 8 == 0 && units % cus == 0) {
+      p.pp_units = (int)units;
+      blocks = (int)cus;
+    }
   } else {
     const int nbh = p.B * p.Hq;
     p.xcd_remap = (nbh % 8 == 0 && (p.B * p.Hkv) % 8 == 0) ? 1 : 0;

@@ -86,6 +86,32 @@ def test_long_causal_row_sample(gpu, s):
     assert m["pass"], m
 
 
+@pytest.mark.parametrize("b,s", [(1, 4096), (2, 4096), (1, 8192)])
+def test_persistent_pairs_cover_every_block(gpu, b, s):
+    """Causal Qwen3 shapes whose (long, short) query-block pairs fill every CU
+    equally run the ping-pong kernel persistently: one workgroup per CU loops
+    over block pairs.  Every output element is written (the output starts as
+    NaN), launches repeat bit for bit, and two rows of every query block pass
+    the oracle gate."""
+    from kernelfuser_amd import attention_prefill, prepare_attention
+    xs = make_inputs(b, s, QWEN3_8B, 4101).to(gpu)
+    kn = torch.empty_like(xs.k)
+    prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+    announce(f"attention persistent pairs B={b} S={s}")
+    outs = []
+    for _ in range(2):
+        out = torch.full_like(xs.q, float("nan"))
+        attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin, causal=True, norm_style="fp32")
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(outs[0]).all())
+    assert torch.equal(outs[0], outs[1])
+    rows = torch.unique(torch.cat([torch.arange(0, s, 128), torch.arange(101, s, 128), torch.tensor([s - 1])]))
+    ref = oracle.oracle_rows_fp32(*[t.cpu() for t in xs.astuple()], rows, True)
+    m = oracle.attention_gate(outs[0][:, :, rows.to(gpu)].cpu(), ref)
+    assert m["pass"], m
+
+
 def test_noncausal_unfused_fp32(gpu):
     xs = make_inputs(2, 300, QWEN3_8B, 1701)
     announce("attention unfused fp32 B=2 S=300 non-causal")
