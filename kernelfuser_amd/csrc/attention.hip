@@ -365,9 +365,9 @@ struct Softmax {
 #pragma unroll
       for (int i = 0; i < 8; ++i) mt[kb * 8 + i] = fmaxf(s[kb][2 * i], s[kb][2 * i + 1]);
 #pragma unroll
-    for (int n = NKB * 4; n >= 1; n >>= 1)
+    for (int n = NKB * 8; n > 1; n = (n + 1) / 2)  // fold the upper ceil half (NKB * 8 need not be 2^k)
 #pragma unroll
-      for (int i = 0; i < n; ++i) mt[i] = fmaxf(mt[i], mt[i + n]);
+      for (int i = 0; i + (n + 1) / 2 < n; ++i) mt[i] = fmaxf(mt[i], mt[i + (n + 1) / 2]);
     float ls[4] = {0.f, 0.f, 0.f, 0.f};  // four interleaved partial sums
     if constexpr (FOLD) {
       const float mx = max_halves(mt[0]);  // tile max of logit - m_run
@@ -448,10 +448,11 @@ __device__ __forceinline__ void gemm1(const unsigned char *smem, int kbuf, const
                                       const bf16x8_t (&qreg)[D / 16], f32x16_t (&s)[BN / 32]) {
   constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16;
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    s[kb] = f32x16_t{};
+  for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16_t{};
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC; ++c) {  // alternating accumulation chains
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
       const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 7] + (c >> 3) * 256);
       s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
     }
@@ -583,12 +584,16 @@ __device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, 
                                            f32x16_t (&o)[D / 32]) {
   constexpr int RB = 2 * D, NKB = BN / 32, NC = D / 16, NK16 = BN / 16, NDB = D / 32;
   constexpr int M1 = NKB * NC, M2 = NK16 * NDB, READS = M1 + (VT ? 1 : 2) * M2, AHEAD = 6;
+  // GEMM1: the key blocks' accumulation chains alternate, so consecutive
+  // MFMAs never depend on each other
 #pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
+  for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[kb][i] = s0;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
       const bf16x8_t a = *reinterpret_cast<const bf16x8_t *>(smem + kbuf + kb * 32 * RB + kra[c & 7] + (c >> 3) * 256);
       s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
     }
