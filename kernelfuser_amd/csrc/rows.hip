@@ -125,11 +125,14 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
+// Heads in flight per lane and the wave count the head chunks aim for,
+// tuned on the six-shape sweep (3 and 12288: +2-3% on the B >= 4 shapes
+// over 2 and 16384, the same at B=1).
 #ifndef KFMI_ROWS_U
-#define KFMI_ROWS_U 2
+#define KFMI_ROWS_U 3
 #endif
 #ifndef KFMI_ROWS_WAVES
-#define KFMI_ROWS_WAVES 16384
+#define KFMI_ROWS_WAVES 12288
 #endif
 #ifndef KFMI_ROWS_NT
 #define KFMI_ROWS_NT 1
@@ -302,7 +305,7 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   const int rpw = 64 / lpr;
   p.n_groups = (int)((a.S + rpw - 1) / rpw);
   const int H = p.Hq_rows + p.Hkv;
-  // Split the heads into chunks so the grid holds >= 8192 waves (32 per CU)
+  // Split the heads into chunks so the grid holds about KFMI_ROWS_WAVES waves
   // when the position count alone does not.
   const int64_t waves = (int64_t)p.B * p.n_groups;
   int chunks = (int)((KFMI_ROWS_WAVES + waves - 1) / waves);
