@@ -627,7 +627,8 @@ __device__ __forceinline__ void mfma_phase(const unsigned char *smem, int kbuf, 
   }
 }
 
-// Epilogue: O = O^T / l as BF16 rows.
+// Epilogue: O = O^T / l as BF16 rows, stored from the registers (8-byte
+// pieces of 32 rows per instruction; used where no LDS staging fits).
 template <int D>
 __device__ __forceinline__ void store_rows(uint16_t *obase, int qrow, bool qvalid, int g, float l_run,
                                            const f32x16_t (&o)[D / 32]) {
@@ -644,6 +645,52 @@ __device__ __forceinline__ void store_rows(uint16_t *obase, int qrow, bool qvali
       wv[1] = pack_bf16x2(o[db][4 * q4 + 2] * rl, o[db][4 * q4 + 3] * rl);
       *reinterpret_cast<u32x2_t *>(orow + 32 * db + 8 * q4 + 4 * g) = wv;
     }
+}
+
+// Epilogue: O = O^T / l as BF16 rows, staged through LDS.  The lane owning
+// query row lr holds 4-column runs of it (columns 32*db + 8*q + 4*g + 0..3);
+// they are written to a row-major tile of the wave's 32 rows (16-byte chunk
+// k of row r in slot k ^ (r % CPR)) and read back as whole chunks, CPR lanes
+// per row, so each global store instruction writes 64 / CPR contiguous rows
+// instead of 8-byte pieces of 32 rows.  `tile` is 32 * 2D bytes of LDS that
+// no other wave touches until the caller's next barrier.  Rows at or past S
+// are not stored.
+template <int D>
+__device__ __forceinline__ void store_rows_lds(unsigned char *tile, uint16_t *obase, int q0, int64_t S, int lane,
+                                               float l_run, const f32x16_t (&o)[D / 32]) {
+  constexpr int RB = 2 * D, CPR = D / 8, RPI = 64 / CPR;
+  const int lr = lane & 31, g = lane >> 5;
+  const float l_tot = sum_halves(l_run);
+  const float rl = __fdiv_rn(1.0f, l_tot);
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      u32x2_t wv;
+      wv[0] = pack_bf16x2(o[db][4 * q4 + 0] * rl, o[db][4 * q4 + 1] * rl);
+      wv[1] = pack_bf16x2(o[db][4 * q4 + 2] * rl, o[db][4 * q4 + 3] * rl);
+      const int k = 4 * db + q4;  // 16-byte chunk of columns 32*db + 8*q4 ..
+      *reinterpret_cast<u32x2_t *>(tile + lr * RB + ((k ^ (lr % CPR)) << 4) + 8 * g) = wv;
+    }
+  // The wave reads back its own writes: the LDS executes one wave's accesses
+  // in issue order, and this keeps the compiler from reordering them.
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  const int c = lane % CPR, rr = lane / CPR;
+  constexpr int NB = 4;  // reads per batch, issued before the batch's row-guarded stores
+#pragma unroll
+  for (int i0 = 0; i0 < 32 / RPI; i0 += NB) {
+    u32x4_t x[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int r = (i0 + i) * RPI + rr;
+      x[i] = *reinterpret_cast<const u32x4_t *>(tile + r * RB + ((c ^ (r % CPR)) << 4));
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int r = (i0 + i) * RPI + rr;
+      if (q0 + r < S) st16(obase + (int64_t)(q0 + r) * D + 8 * c, x[i]);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -815,7 +862,8 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     }
   }
 
-  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+  __syncthreads();  // both groups are past their last reads of the K/V buffers
+  store_rows_lds<D>(smem + w * (32 * 2 * D), p.out + qoff * D, q0, S, lane, sm.l_run, o);
   };
 
   // ---- work items.  Persistent (pp_units > 0, causal): workgroup bid takes
@@ -1020,7 +1068,13 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
 
   // the host plans splits for D = 256 only (plan_split)
   if (D != 256 || sid < 0) {
-    store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+    if constexpr (FK) {
+      // mode 'full' runs at the register limit: direct stores
+      store_rows<D>(p.out + qoff * D, qrow, qvalid, g, sm.l_run, o);
+    } else {
+      __syncthreads();  // the K/V buffers become the epilogue's staging tiles
+      store_rows_lds<D>(smem + w * (32 * 2 * D), p.out + qoff * D, q0, S, lane, sm.l_run, o);
+    }
     return;
   }
   // ---- one half of a split query block: publish the partial state (O
@@ -1080,7 +1134,8 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     }
   }
   const float l0 = part == 0 ? sm.l_run : lo, l1 = part == 0 ? lo : sm.l_run;
-  store_rows<D>(p.out + qoff * D, qrow, qvalid, g, fmaf(l0, a0, l1 * a1), o);
+  __syncthreads();
+  store_rows_lds<D>(smem + w * (32 * 2 * D), p.out + qoff * D, q0, S, lane, fmaf(l0, a0, l1 * a1), o);
   if (tid == 0) atomicExch(p.counters + pair, 0);
 }
 
