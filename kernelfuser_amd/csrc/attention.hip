@@ -225,9 +225,17 @@ __device__ __forceinline__ void lds_read_offsets(int lane, uint32_t (&kra)[8], u
 // FOLD (FP32 style with a norm prologue only): the logit multiplier is
 // applied to the normalised FP32 row before its single rounding, so the MFMA
 // yields scores already in log2 units and cl becomes 1.
+// Rotary table rows staged in LDS by the caller (tab == nullptr: read from
+// global memory): the lane's chunk 2c+g of cos is at cos + off[c], of sin at
+// sin + off[c]; the copies are waited for at the barrier inside q_prologue.
+struct StagedTables {
+  const unsigned char *cos = nullptr, *sin = nullptr;
+  const uint32_t *off = nullptr;
+};
+
 template <int D, int PRO, int ST, bool FOLD = false>
 __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, int qrow, bool qvalid, int g,
-                                           bf16x8_t (&qreg)[D / 16], float &cl) {
+                                           bf16x8_t (&qreg)[D / 16], float &cl, const StagedTables tab = {}) {
   constexpr int NC = D / 16;
   const uint16_t *qbase = p.q + qoff * D;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
@@ -253,11 +261,13 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
       for (int c = 0; c < NC; ++c) graw[c] = ld16(p.gq + 16 * c + 8 * g);
     }
     if constexpr (TAB) {
-      const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
+      if (tab.cos == nullptr) {
+        const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        craw[c] = ld16(p.cos + trow + 16 * c + 8 * g);
-        sraw[c] = ld16(p.sin + trow + 16 * c + 8 * g);
+        for (int c = 0; c < NC; ++c) {
+          craw[c] = ld16(p.cos + trow + 16 * c + 8 * g);
+          sraw[c] = ld16(p.sin + trow + 16 * c + 8 * g);
+        }
       }
     }
     float ss = 0.f;
@@ -270,6 +280,17 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
     }
     ss = sum_halves(ss);
     const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+    if constexpr (TAB) {
+      if (tab.cos != nullptr) {  // workgroup-uniform
+        wait_copies();
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          craw[c] = *reinterpret_cast<const u32x4_t *>(tab.cos + tab.off[c]);
+          sraw[c] = *reinterpret_cast<const u32x4_t *>(tab.sin + tab.off[c]);
+        }
+      }
+    }
     if constexpr (PRO == PRO_FACTORED_CALC) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) qreg[c] = as_bf16x8(raw[c]);
@@ -703,8 +724,12 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   constexpr int LPW = TILE / 1024 / 8;  // copies per wave per tile (2)
   constexpr int NC = D / 16, NDB = D / 32, NKB = BN / 32, NK16 = BN / 16;
   constexpr int K0 = 0, K1 = TILE, V0 = 2 * TILE, V1 = 3 * TILE;
+  // Rotary table rows of the block's BM positions (cos, then sin), shared by
+  // both heads: staged with coalesced copies instead of 32 rows per load.
+  constexpr int TROWS = 4 * TILE, TAB_BYTES = BM * 2 * D;
+  constexpr bool STAGE_TAB = PRO == PRO_NORM_ROPE;
 
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE + (STAGE_TAB ? 2 * TAB_BYTES : 0)];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -769,13 +794,31 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 
   copy_k(0, K0);
 
+  uint32_t kra[8], vra[4];
+  lds_read_offsets<D>(lane, kra, vra);
+  StagedTables tab;
+  if constexpr (STAGE_TAB) {
+    // wave w copies rows 16w .. 16w+15 of each table, 4 rows per copy, with
+    // the K tiles' chunk swizzle, so kra[c] addresses the lane's row chunk
+    const i32x4_t crs = buffer_rsrc(p.cos, (uint32_t)(S * 2 * D));
+    const i32x4_t srs = buffer_rsrc(p.sin, (uint32_t)(S * 2 * D));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * w + i;
+      const uint32_t voff = copy_lane_offset<D>(j, lane, false);
+      const uint32_t soff = (uint32_t)(((int64_t)qb * BM + 4 * j) * 2 * D);
+      copy16_to_lds(crs, lds0 + TROWS + j * 1024, voff, soff);
+      copy16_to_lds(srs, lds0 + TROWS + TAB_BYTES + j * 1024, voff, soff);
+    }
+    tab.cos = smem + TROWS + wq * 32 * 2 * D;
+    tab.sin = tab.cos + TAB_BYTES;
+    tab.off = kra;
+  }
+
   constexpr bool FOLD = ST == ST_FP32 && (PRO == PRO_NORM || PRO == PRO_NORM_ROPE);
   bf16x8_t qreg[NC];
   float cl;
-  q_prologue<D, PRO, ST, FOLD>(p, qoff, qrow, qvalid, g, qreg, cl);
-
-  uint32_t kra[8], vra[4];
-  lds_read_offsets<D>(lane, kra, vra);
+  q_prologue<D, PRO, ST, FOLD>(p, qoff, qrow, qvalid, g, qreg, cl, tab);
   if constexpr (VT) {
     // V^T reads: row 32*db + lr, chunk 2*c2 + g, swizzled by (row >> 1) & 7.
 #pragma unroll
