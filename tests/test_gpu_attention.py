@@ -86,18 +86,20 @@ def test_long_causal_row_sample(gpu, s):
     assert m["pass"], m
 
 
-@pytest.mark.parametrize("b,s", [(1, 4096), (2, 4096), (1, 8192)])
-def test_persistent_pairs_cover_every_block(gpu, b, s):
+@pytest.mark.parametrize("b,s,geom", [(1, 4096, QWEN3_8B), (2, 4096, QWEN3_8B), (1, 8192, QWEN3_8B),
+                                      (1, 8192, (16, 8, 128)), (1, 4096, (64, 8, 128))])
+def test_persistent_pairs_cover_every_block(gpu, b, s, geom):
     """Causal Qwen3 shapes whose (long, short) query-block pairs fill every CU
     equally run the ping-pong kernel persistently: one workgroup per CU loops
     over block pairs.  Every output element is written (the output starts as
     NaN), launches repeat bit for bit, and two rows of every query block pass
     the oracle gate."""
     from kernelfuser_amd import attention_prefill, prepare_attention
-    xs = make_inputs(b, s, QWEN3_8B, 4101).to(gpu)
+    # GQA ratios 4 (two head pairs per KV head), 2 (one) and 8 (four)
+    xs = make_inputs(b, s, geom, 4101).to(gpu)
     kn = torch.empty_like(xs.k)
     prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
-    announce(f"attention persistent pairs B={b} S={s}")
+    announce(f"attention persistent pairs B={b} S={s} geometry={geom}")
     outs = []
     for _ in range(2):
         out = torch.full_like(xs.q, float("nan"))
