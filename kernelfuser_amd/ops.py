@@ -67,12 +67,15 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 
 # ---------------------------------------------------------------------------
 # Split-KV workspace (see kfmi_attention_workspace_bytes): one zero-filled
-# buffer per device, grown on demand outside graph capture; each launch leaves
-# its counters at zero again.  Launches on one device share it, so they must
-# run in stream order (as torch's current stream does).
+# buffer per (device, stream), grown on demand outside graph capture; each
+# launch leaves its counters at zero again.  Launches that share a buffer run
+# in their stream's order, so launches on different streams never overlap on
+# one buffer.  A capture uses the buffer its stream already holds (warm-up
+# launches on that stream allocate it); without one the captured launch does
+# not split.
 # ---------------------------------------------------------------------------
 
-_work_cache: dict[int, torch.Tensor] = {}
+_work_cache: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def attention_workspace_bytes(b: int, hq: int, hkv: int, s: int, d: int, causal: bool) -> int:
@@ -85,18 +88,21 @@ def attention_workspace_bytes(b: int, hq: int, hkv: int, s: int, d: int, causal:
 
 
 def _workspace(device: torch.device, nbytes: int):
-    """The device's cached workspace of at least nbytes, or None (no split)
-    when it would have to be allocated during graph capture."""
+    """The current stream's cached workspace of at least nbytes on this
+    device, or None (no split) when it would have to be allocated during graph
+    capture."""
     if nbytes <= 0:
         return None
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    buf = _work_cache.get(idx)
+    stream = torch.cuda.current_stream(torch.device("cuda", idx))
+    key = (idx, stream.cuda_stream)
+    buf = _work_cache.get(key)
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             return None
         buf = torch.zeros(max(nbytes, 0 if buf is None else 2 * buf.numel()), dtype=torch.uint8, device=device)
-        torch.cuda.current_stream(device).synchronize()
-        _work_cache[idx] = buf
+        stream.synchronize()
+        _work_cache[key] = buf
     return buf
 
 

@@ -86,3 +86,27 @@ def test_split_graph_replays(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
 
+
+
+def test_split_cached_workspace_per_stream(gpu):
+    """With work=None each (device, stream) gets its own cached workspace, so
+    split launches on two streams at once do not share counters or partials:
+    both streams reproduce the single-stream result bit for bit."""
+    xs = make_inputs(1, 2048, (16, 8, 256), 1515).to(gpu)
+    kn = torch.empty_like(xs.k)
+    prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+    announce("split cached workspace on two streams")
+    ref = _run(xs, kn, True, None)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.empty_like(xs.q) for _ in streams]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for _ in range(4):
+        for st, out in zip(streams, outs):
+            with torch.cuda.stream(st):
+                attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin, causal=True,
+                                  norm_style="fp32")
+    torch.cuda.synchronize()
+    for out in outs:
+        assert torch.equal(out, ref)
