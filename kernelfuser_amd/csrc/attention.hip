@@ -63,6 +63,8 @@
 // longest query blocks first.
 #include <math.h>
 
+#include <atomic>
+
 #include "kfmi_device.h"
 #include "kfmi_launch.h"
 
@@ -1239,14 +1241,16 @@ namespace {
 // 256 when no device can be queried.  Scheduling only: results never depend
 // on it.
 int64_t device_cus() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64];  // 0: not queried yet (host threads may race; every writer stores the same value)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     int n = 0;
-    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    v = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 // Split-KV plan for the general kernel at D = 256, which runs one workgroup
