@@ -235,9 +235,16 @@ struct StagedTables {
   const uint32_t *off = nullptr;
 };
 
-template <int D, int PRO, int ST, bool FOLD = false>
+struct NoOp {
+  __device__ void operator()() const {}
+};
+
+// after_tab() runs once the staged table rows are in registers (after a
+// barrier), before the normalisation and rotation arithmetic.
+template <int D, int PRO, int ST, bool FOLD = false, typename AfterTab = NoOp>
 __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, int qrow, bool qvalid, int g,
-                                           bf16x8_t (&qreg)[D / 16], float &cl, const StagedTables tab = {}) {
+                                           bf16x8_t (&qreg)[D / 16], float &cl, const StagedTables tab = {},
+                                           AfterTab after_tab = {}) {
   constexpr int NC = D / 16;
   const uint16_t *qbase = p.q + qoff * D;
   const u32x4_t zero = {0u, 0u, 0u, 0u};
@@ -291,6 +298,7 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
           craw[c] = *reinterpret_cast<const u32x4_t *>(tab.cos + tab.off[c]);
           sraw[c] = *reinterpret_cast<const u32x4_t *>(tab.sin + tab.off[c]);
         }
+        after_tab();
       }
     }
     if constexpr (PRO == PRO_FACTORED_CALC) {
@@ -1052,17 +1060,51 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   const int nTw0 = q0 < S ? (int)((wave_end + BN - 1) / BN) : 0;  // tiles with any unmasked key
   const int nTw = nTw0 < nT ? nTw0 : nT;
 
-  // Start the first copies before the prologue's own global loads.
-  copy_k(t0, K0);
-  copy_v(t0, V0);
-  if (t0 + 1 < nT) copy_k(t0 + 1, K1);
+  uint32_t kra[8], vra[4];
+  lds_read_offsets<D>(lane, kra, vra);
+
+  auto first_copies = [&]() {
+    copy_k(t0, K0);
+    copy_v(t0, V0);
+    if (t0 + 1 < nT) copy_k(t0 + 1, K1);
+  };
+  // D = 128 with RoPE: the rotary-table rows of the wave's 32 positions are
+  // first staged in the K/V buffers (cos in the first 32 KiB, sin in the
+  // second) with coalesced copies (8 per table per wave, the K tiles' chunk
+  // swizzle, so kra[c] addresses the lane's chunks) instead of loads that
+  // each touch 32 rows.  Once every wave holds its rows in registers the
+  // first K/V copies are issued; they land while the prologue computes.
+  constexpr bool STAGE_TAB = D == 128 && PRO == PRO_NORM_ROPE && !FK;
+  StagedTables tab;
+  if constexpr (STAGE_TAB) {
+    const i32x4_t crs = buffer_rsrc(p.cos, (uint32_t)(S * RB));
+    const i32x4_t srs = buffer_rsrc(p.sin, (uint32_t)(S * RB));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int j = 8 * w + i;  // rows 4j .. 4j+3 of the block
+      const uint32_t voff = copy_lane_offset<D>(j, lane, false);
+      const uint32_t soff = (uint32_t)(((int64_t)qb * BM + 4 * j) * RB);
+      copy16_to_lds(crs, lds0 + j * 1024, voff, soff);
+      copy16_to_lds(srs, lds0 + 32768 + j * 1024, voff, soff);
+    }
+    tab.cos = smem + w * 32 * RB;
+    tab.sin = tab.cos + 32768;
+    tab.off = kra;
+  } else {
+    // Start the first copies before the prologue's own global loads.
+    first_copies();
+  }
 
   bf16x8_t qreg[NC];
   float cl;
-  q_prologue<D, PRO, ST>(p, qoff, qrow, qvalid, g, qreg, cl);
-
-  uint32_t kra[8], vra[4];
-  lds_read_offsets<D>(lane, kra, vra);
+  if constexpr (STAGE_TAB) {
+    q_prologue<D, PRO, ST>(p, qoff, qrow, qvalid, g, qreg, cl, tab, [&]() {
+      __syncthreads();  // every wave's table reads have completed
+      first_copies();
+    });
+  } else {
+    q_prologue<D, PRO, ST>(p, qoff, qrow, qvalid, g, qreg, cl);
+  }
 
   f32x16_t o[NDB];
 #pragma unroll
