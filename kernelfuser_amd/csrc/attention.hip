@@ -227,9 +227,12 @@ __device__ __forceinline__ void lds_read_offsets(int lane, uint32_t (&kra)[8], u
 // FOLD (FP32 style with a norm prologue only): the logit multiplier is
 // applied to the normalised FP32 row before its single rounding, so the MFMA
 // yields scores already in log2 units and cl becomes 1.
-// Rotary table rows staged in LDS by the caller (tab == nullptr: read from
+// Rotary table rows staged in LDS by the caller (STAGED; otherwise read from
 // global memory): the lane's chunk 2c+g of cos is at cos + off[c], of sin at
 // sin + off[c]; the copies are waited for at the barrier inside q_prologue.
+// STAGED is a template parameter, not a null test of tab.cos, so that the
+// unused global-load path is not compiled in (its loads, though never
+// executed, made the compiler add waits for them).
 struct StagedTables {
   const unsigned char *cos = nullptr, *sin = nullptr;
   const uint32_t *off = nullptr;
@@ -241,7 +244,7 @@ struct NoOp {
 
 // after_tab() runs once the staged table rows are in registers (after a
 // barrier), before the normalisation and rotation arithmetic.
-template <int D, int PRO, int ST, bool FOLD = false, typename AfterTab = NoOp>
+template <int D, int PRO, int ST, bool FOLD = false, bool STAGED = false, typename AfterTab = NoOp>
 __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, int qrow, bool qvalid, int g,
                                            bf16x8_t (&qreg)[D / 16], float &cl, const StagedTables tab = {},
                                            AfterTab after_tab = {}) {
@@ -270,7 +273,7 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
       for (int c = 0; c < NC; ++c) graw[c] = ld16(p.gq + 16 * c + 8 * g);
     }
     if constexpr (TAB) {
-      if (tab.cos == nullptr) {
+      if constexpr (!STAGED) {
         const int64_t trow = qvalid ? (int64_t)qrow * D : 0;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -290,7 +293,7 @@ __device__ __forceinline__ void q_prologue(const AttnParams &p, int64_t qoff, in
     ss = sum_halves(ss);
     const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
     if constexpr (TAB) {
-      if (tab.cos != nullptr) {  // workgroup-uniform
+      if constexpr (STAGED) {
         wait_copies();
         __syncthreads();
 #pragma unroll
@@ -828,7 +831,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   constexpr bool FOLD = ST == ST_FP32 && (PRO == PRO_NORM || PRO == PRO_NORM_ROPE);
   bf16x8_t qreg[NC];
   float cl;
-  q_prologue<D, PRO, ST, FOLD>(p, qoff, qrow, qvalid, g, qreg, cl, tab);
+  q_prologue<D, PRO, ST, FOLD, STAGE_TAB>(p, qoff, qrow, qvalid, g, qreg, cl, tab);
   if constexpr (VT) {
     // V^T reads: row 32*db + lr, chunk 2*c2 + g, swizzled by (row >> 1) & 7.
 #pragma unroll
@@ -1098,7 +1101,7 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   bf16x8_t qreg[NC];
   float cl;
   if constexpr (STAGE_TAB) {
-    q_prologue<D, PRO, ST>(p, qoff, qrow, qvalid, g, qreg, cl, tab, [&]() {
+    q_prologue<D, PRO, ST, false, true>(p, qoff, qrow, qvalid, g, qreg, cl, tab, [&]() {
       __syncthreads();  // every wave's table reads have completed
       first_copies();
     });
