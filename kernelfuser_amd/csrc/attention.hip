@@ -82,6 +82,11 @@ struct AttnParams {
   // ping-pong kernel, persistent mode: number of (long, short) query-block
   // pairs; 0 = one item per workgroup
   int pp_units;
+  // general kernel, causal, one round of two workgroups per CU (slot2 = the
+  // CU count, > 0): workgroups bid and bid + slot2 share a CU, so the second
+  // slot takes the query blocks shortest first and each CU's pair sums to
+  // the same number of key tiles
+  int slot2;
   float c_scale;  // scale*log2(e); for the factored prologues D^-1/2*log2(e)
   float eps;
   // Split-KV plan of the general kernel (n_items > 0): work item r of the
@@ -1006,6 +1011,8 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     t0 = p.it_t0[rank];
     t1 = p.it_t1[rank];
     sid = p.it_sid[rank];
+  } else if (CAUSAL && p.slot2 > 0 && bid >= p.slot2) {
+    qb = (bid - p.slot2) / nbh;
   } else {
     qb = CAUSAL ? p.n_qblocks - 1 - rank : rank;
   }
@@ -1368,6 +1375,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   AttnParams p;
   p.n_items = 0;
   p.pp_units = 0;
+  p.slot2 = 0;
   p.counters = nullptr;
   p.partials = nullptr;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
@@ -1414,6 +1422,12 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
         blocks = pl.n_items * nbh;
       }
     }
+    // D = 128, causal, all workgroups resident in one round of two per CU:
+    // pair each CU's long block with a short one (the head stays the same,
+    // as bid and bid + cus map to the same head when cus % nbh == 0)
+    const int64_t cus = device_cus();
+    if (a.causal && a.D == 128 && p.n_items == 0 && cus % nbh == 0 && blocks > cus && blocks <= 2 * cus)
+      p.slot2 = (int)cus;
   }
   if (a.D == 128) {
     return a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, pp, blocks, stream)

@@ -86,6 +86,21 @@ def test_long_causal_row_sample(gpu, s):
     assert m["pass"], m
 
 
+@pytest.mark.parametrize("b,s", [(1, 1900), (2, 1024)])
+def test_two_slot_pairs_row_sample(gpu, b, s):
+    """Causal D=128 grids that fill exactly one round of two workgroups per CU
+    pair each CU's long query block with a short one (the second slot runs
+    shortest first): R = 15 blocks at B=1, S=1900 (a ragged tail), and
+    B=2, S=1024.  Two rows of every query block pass the oracle gate."""
+    xs = make_inputs(b, s, QWEN3_8B, 3303)
+    announce(f"attention query fp32 B={b} S={s} causal (two-slot pairs)")
+    out = _run(xs.to(gpu), True)
+    rows = torch.unique(torch.cat([torch.arange(0, s, 128), torch.arange(77, s, 128), torch.tensor([s - 1])]))
+    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
+    m = oracle.attention_gate(out[:, :, rows], ref)
+    assert m["pass"], m
+
+
 @pytest.mark.parametrize("b,s,geom", [(1, 4096, QWEN3_8B), (2, 4096, QWEN3_8B), (1, 8192, QWEN3_8B),
                                       (1, 8192, (16, 8, 128)), (1, 4096, (64, 8, 128))])
 def test_persistent_pairs_cover_every_block(gpu, b, s, geom):
