@@ -86,6 +86,22 @@ def test_long_causal_row_sample(gpu, s):
     assert m["pass"], m
 
 
+@pytest.mark.parametrize("geom,b,s", [((32, 4, 128), 1, 3072), ((32, 8, 128), 3, 4096), ((8, 2, 128), 2, 3200)])
+def test_pp_geometries_row_sample(gpu, geom, b, s):
+    """Ping-pong kernel shapes off the Qwen3 grid: KV heads that do not
+    spread evenly over the 8 XCDs (B*Hkv = 4: heads in plain order, one item
+    per workgroup; ragged S=3200), and three block pairs per CU in the
+    persistent loop (B=3, S=4096).  Two rows of every query block pass the
+    oracle gate."""
+    xs = make_inputs(b, s, geom, 5151)
+    announce(f"attention query fp32 geometry={geom} B={b} S={s} causal (ping-pong)")
+    out = _run(xs.to(gpu), True)
+    rows = torch.unique(torch.cat([torch.arange(0, s, 128), torch.arange(93, s, 128), torch.tensor([s - 1])]))
+    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
+    m = oracle.attention_gate(out[:, :, rows], ref)
+    assert m["pass"], m
+
+
 @pytest.mark.parametrize("b,s", [(1, 1900), (2, 1024)])
 def test_two_slot_pairs_row_sample(gpu, b, s):
     """Causal D=128 grids that fill exactly one round of two workgroups per CU
