@@ -57,6 +57,9 @@ def parse_args():
     ap.add_argument("--quick", action="store_true", help="headline workload only (no sweep, extra shapes, CPU)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline budget per workload")
+    ap.add_argument("--sweep-only", action="store_true",
+                    help="only the norm+RoPE six-shape sweep (for a kernel-trace profile of rows_kernel); prints "
+                         "a JSON line with the sweep")
     ap.add_argument("--pmc", action="store_true",
                     help="short run for rocprofv3 counter passes: a few launches of each kernel plus a "
                          "copy of known size for calibration; prints a JSON line of what ran")
@@ -299,6 +302,9 @@ def main():
     _lib.load()
     if args.pmc:
         pmc_run(torch, kf)
+        return
+    if args.sweep_only:
+        print(json.dumps({"norm_rope": norm_rope_sweep(args, torch, kf)}), flush=True)
         return
     head, xs_cpu, out = headline(args, torch, kf)
     traffic = load_traffic().get("attention_b%d_s%d" % (args.batch, args.seq))
