@@ -41,8 +41,10 @@
 // K/V staging: tiles of BN rows (16 KiB each) are copied HBM -> LDS by the
 // buffer unit (buffer_load_dwordx4 ... lds: lane L of a copy writes LDS bytes
 // base + 16*L), so no VGPRs, no ds_write and no bounds branches are spent on
-// staging: rows past S lie outside the buffer descriptor's range and arrive as
-// zeros.  Both K and V are double-buffered; the 16-byte chunks of each row are
+// staging: each copy's full byte offset is its VGPR offset, which the raw-buffer
+// range check covers, and the descriptor spans exactly one head's S rows, so
+// rows past S arrive as zeros (never the next head's or another allocation's
+// bytes).  Both K and V are double-buffered; the 16-byte chunks of each row are
 // XOR-swizzled (K: chunk ^ (row & 15); V: chunk ^ 4*(row & 3)) so that the 16
 // lanes of a GEMM1 row read (16 B each) and the 32 lanes of a GEMM2 transpose
 // read (8 B each) cover all 64 LDS banks exactly once.
@@ -134,18 +136,21 @@ __device__ __forceinline__ i32x4_t buffer_rsrc(const void *base, uint32_t bytes)
   return r;
 }
 
-// 16 bytes per lane from buffer offset voff + soff into LDS at lds + 16*lane.
+// 16 bytes per lane from buffer byte offset voff into LDS at lds + 16*lane.
+// The whole offset travels in the VGPR operand (the SGPR offset is the
+// constant 0): the raw-buffer range check compares voffset + the instruction
+// offset with num_records, so a chunk at or past the descriptor's size reads
+// as zeros whatever the hardware does with a non-zero SGPR offset.
 // Issued as inline assembly so the compiler does not guard every later LDS
 // read with a wait for it; the kernels order copies and reads themselves
 // (wait_copies + barrier).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; it is set right here
-__device__ __forceinline__ void copy16_to_lds(const i32x4_t &rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  // lds and soff are wave-uniform; readfirstlane pins them to SGPRs.
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+__device__ __forceinline__ void copy16_to_lds(const i32x4_t &rsrc, uint32_t lds, uint32_t voff) {
+  // lds is wave-uniform; readfirstlane pins it to an SGPR.
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc),
-                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -196,16 +201,16 @@ __device__ __forceinline__ void fence_in(bf16x8_t (&x)[N]) {
 #endif
 }
 
-// Source offset (bytes, within the head's rows) of the chunk that copy `inst`
-// places in LDS slot lane%CPR of row inst*RPI + lane/CPR, for the K or V
-// swizzle.  The copy's own row offset inst*1024 is added as soffset.
+// Source offset (bytes, from the first row of the tile) of the chunk that
+// copy `inst` places in LDS slot lane%CPR of row inst*RPI + lane/CPR, for the
+// K or V swizzle.  The caller adds the tile's own row offset.
 template <int D>
 __device__ __forceinline__ uint32_t copy_lane_offset(int inst, int lane, bool v_tile) {
   constexpr int RB = 2 * D, CPR = D / 8, RPI = 1024 / RB;
   const int row = inst * RPI + lane / CPR;
   const int slot = lane % CPR;
   const int chunk = v_tile ? (slot ^ ((row & 3) << 2)) : (slot ^ (row & 15));
-  return (uint32_t)((lane / CPR) * RB + (chunk << 4));
+  return (uint32_t)(row * RB + (chunk << 4));
 }
 
 // Per-lane LDS read offsets.  GEMM1: lane reads row 32*kb + lr, chunk 2c + g;
@@ -783,7 +788,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
       // VT tile: copy inst fills V^T rows 8*inst + lane/8 (2*BN = 128 bytes of
       // keys each), slot lane%8, swizzle chunk ^ ((row >> 1) & 7).
       const int row = 8 * inst + lane / 8;
-      vvo[i] = (uint32_t)((lane / 8) * S * 2 + (((lane % 8) ^ ((row >> 1) & 7)) << 4));
+      vvo[i] = (uint32_t)(row * S * 2 + (((lane % 8) ^ ((row >> 1) & 7)) << 4));
     } else {
       vvo[i] = copy_lane_offset<D>(inst, lane, true);
     }
@@ -792,15 +797,14 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int inst = w * LPW + i;
-      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i], (uint32_t)(t * TILE + inst * 1024));
+      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i] + (uint32_t)(t * TILE));
     }
   };
   auto copy_v = [&](int t, int buf) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int inst = w * LPW + i;
-      const uint32_t soff = VT ? (uint32_t)(inst * 8 * S * 2 + t * 2 * BN) : (uint32_t)(t * TILE + inst * 1024);
-      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], soff);
+      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i] + (uint32_t)(VT ? t * 2 * BN : t * TILE));
     }
   };
 
@@ -823,10 +827,9 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * w + i;
-      const uint32_t voff = copy_lane_offset<D>(j, lane, false);
-      const uint32_t soff = (uint32_t)(((int64_t)qb * BM + 4 * j) * 2 * D);
-      copy16_to_lds(crs, lds0 + TROWS + j * 1024, voff, soff);
-      copy16_to_lds(srs, lds0 + TROWS + TAB_BYTES + j * 1024, voff, soff);
+      const uint32_t voff = copy_lane_offset<D>(j, lane, false) + (uint32_t)(qb * BM * 2 * D);
+      copy16_to_lds(crs, lds0 + TROWS + j * 1024, voff);
+      copy16_to_lds(srs, lds0 + TROWS + TAB_BYTES + j * 1024, voff);
     }
     tab.cos = smem + TROWS + wq * 32 * 2 * D;
     tab.sin = tab.cos + TAB_BYTES;
@@ -1048,14 +1051,14 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int inst = w * LPW + i;
-      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i], (uint32_t)(t * TILE + inst * 1024));
+      copy16_to_lds(krs, lds0 + buf + inst * 1024, kvo[i] + (uint32_t)(t * TILE));
     }
   };
   auto copy_v = [&](int t, int buf) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int inst = w * LPW + i;
-      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i], (uint32_t)(t * TILE + inst * 1024));
+      copy16_to_lds(vrs, lds0 + buf + inst * 1024, vvo[i] + (uint32_t)(t * TILE));
     }
   };
 
@@ -1092,10 +1095,9 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int j = 8 * w + i;  // rows 4j .. 4j+3 of the block
-      const uint32_t voff = copy_lane_offset<D>(j, lane, false);
-      const uint32_t soff = (uint32_t)(((int64_t)qb * BM + 4 * j) * RB);
-      copy16_to_lds(crs, lds0 + j * 1024, voff, soff);
-      copy16_to_lds(srs, lds0 + 32768 + j * 1024, voff, soff);
+      const uint32_t voff = copy_lane_offset<D>(j, lane, false) + (uint32_t)(qb * BM * RB);
+      copy16_to_lds(crs, lds0 + j * 1024, voff);
+      copy16_to_lds(srs, lds0 + 32768 + j * 1024, voff);
     }
     tab.cos = smem + w * 32 * RB;
     tab.sin = tab.cos + 32768;

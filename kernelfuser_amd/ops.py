@@ -66,42 +66,54 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 
 
 # ---------------------------------------------------------------------------
-# Split-KV workspace (see kfmi_attention_workspace_bytes): one zero-filled
-# buffer per (device, stream), grown on demand outside graph capture; each
-# launch leaves its counters at zero again.  Launches that share a buffer run
-# in their stream's order, so launches on different streams never overlap on
-# one buffer.  A capture uses the buffer its stream already holds (warm-up
-# launches on that stream allocate it); without one the captured launch does
-# not split.
+# Split-KV workspace (see kfmi_attention_workspace_bytes).  Eager launches use
+# one zero-filled buffer per (device, stream); launches that share it run in
+# that stream's order, so they never overlap on it, and each launch leaves
+# its counters at zero again.  When a larger shape needs more, a new buffer
+# replaces it in the cache; the old one stays referenced until the process
+# ends, so nothing that ever held its address sees it freed.  A launch
+# captured into a HIP graph never uses the cache: it gets its own zero-filled
+# buffer from the graph's private memory pool (the fill is part of the graph
+# and runs before the launch on every replay), so replays, on whatever
+# stream, never share a workspace with eager launches or with other graphs.
 # ---------------------------------------------------------------------------
 
 _work_cache: dict[tuple[int, int], torch.Tensor] = {}
+_work_retired: list[torch.Tensor] = []
+_work_bytes_cache: dict[tuple, int] = {}
 
 
 def attention_workspace_bytes(b: int, hq: int, hkv: int, s: int, d: int, causal: bool) -> int:
     """Workspace bytes with which attention splits the longest causal query
-    blocks over two workgroups for this shape (0: it never splits)."""
-    n = int(_lib.load().kfmi_attention_workspace_bytes(b, hq, hkv, s, d, int(bool(causal))))
-    if n < 0:
-        raise ValueError("invalid attention shape")
+    blocks over two workgroups for this shape on the current device (0: it
+    never splits).  Cached per (device, shape)."""
+    key = (torch.cuda.current_device() if torch.cuda.is_available() else -1, b, hq, hkv, s, d, bool(causal))
+    n = _work_bytes_cache.get(key)
+    if n is None:
+        n = int(_lib.load().kfmi_attention_workspace_bytes(b, hq, hkv, s, d, int(bool(causal))))
+        if n < 0:
+            raise ValueError("invalid attention shape")
+        _work_bytes_cache[key] = n
     return n
 
 
 def _workspace(device: torch.device, nbytes: int):
-    """The current stream's cached workspace of at least nbytes on this
-    device, or None (no split) when it would have to be allocated during graph
-    capture."""
+    """A zero-filled workspace of at least nbytes on this device: the current
+    stream's cached one for eager launches, a new one from the graph's pool
+    during capture; None when nbytes is 0."""
     if nbytes <= 0:
         return None
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     stream = torch.cuda.current_stream(torch.device("cuda", idx))
     key = (idx, stream.cuda_stream)
     buf = _work_cache.get(key)
     if buf is None or buf.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
-            return None
+        if buf is not None:
+            _work_retired.append(buf)
+        # zero-filled on the stream the launches run on, so in their order
         buf = torch.zeros(max(nbytes, 0 if buf is None else 2 * buf.numel()), dtype=torch.uint8, device=device)
-        stream.synchronize()
         _work_cache[key] = buf
     return buf
 
@@ -382,6 +394,10 @@ def norm_rope(q, k, gq, gk, cos=None, sin=None, *, norm_style="fp32", qn=None, k
     if tuple(gq.shape) != (d,) or tuple(gk.shape) != (d,) or (cos is not None and (
             tuple(cos.shape) != (s, d) or tuple(sin.shape) != (s, d))):
         raise ValueError("Expected gamma vectors [D] and optional rotary tables [S,D]")
+    for name, out, like in (("qn", qn, q), ("kn", kn, k)):
+        if out is not None and (out.shape != like.shape or out.dtype != torch.bfloat16
+                                or out.device != like.device or not out.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous BF16 tensor shaped like its input on the same device")
     tensors = (q, k, gq, gk) + ((cos, sin) if cos is not None else ())
     _check_device(tensors, q.device)
     if qn is None and kn is None:

@@ -114,6 +114,25 @@ def test_norm_rope_rules(xs):
         kf.norm_rope(xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)
 
 
+@pytest.mark.parametrize("which", ["qn", "kn"])
+@pytest.mark.parametrize("bad", ["short", "dtype", "strided", "other_shape"])
+def test_norm_rope_output_buffers(xs, which, bad):
+    """Caller-supplied outputs are checked (shape, BF16, device, contiguity)
+    before anything else, so a too-small or strided buffer never reaches the
+    kernel."""
+    like = xs.q if which == "qn" else xs.k
+    b, h, s, d = like.shape
+    buf = {"short": torch.empty(b, h, s - 1, d, dtype=torch.bfloat16),
+           "dtype": torch.empty_like(like, dtype=torch.float32),
+           "strided": torch.empty(b, h, d, s, dtype=torch.bfloat16).transpose(2, 3),
+           "other_shape": torch.empty(b, h + 1, s, d, dtype=torch.bfloat16)}[bad]
+    with pytest.raises(ValueError, match=f"{which} must be a contiguous BF16 tensor shaped like"):
+        kf.norm_rope(xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin, **{which: buf})
+    # well-formed buffers pass this rule and stop at the device rule (CPU tensors)
+    with pytest.raises(ValueError, match="one GPU device"):
+        kf.norm_rope(xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin, **{which: torch.empty_like(like)})
+
+
 def test_factored_rules(xs):
     with pytest.raises(ValueError, match="Expected"):
         kf.factored_qk_attention(xs.q, xs.k, xs.v[:, :1], xs.gq, xs.gk)

@@ -35,6 +35,32 @@ def test_config3_s2048_causal_fp32(gpu):
     assert m["pass"], m
 
 
+@pytest.mark.parametrize("b,s", [(1, 2048), (4, 1000)])
+def test_default_hf_style_configs_3_4(gpu, b, s):
+    """The default norm_style ('hf', rope:680-681) at config 3 (B=1, S=2048) and
+    the ragged config-4 case (B=4, S=1000), whole output, under the reference
+    metric (rope:287-293) against the FP32 oracle."""
+    xs = make_inputs(b, s, QWEN3_8B, 1909)
+    announce(f"attention query hf B={b} S={s} causal")
+    out = _run(xs.to(gpu), True, norm_style="hf")
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.metric(out, ref)
+    assert m["pass"], m
+
+
+@pytest.mark.parametrize("s", [4096, 8192])
+def test_default_hf_style_long_row_sample(gpu, s):
+    """The default 'hf' style on the ping-pong kernel (config 4 long shapes):
+    a row sample incl. first and last rows under the reference metric."""
+    xs = make_inputs(1, s, QWEN3_8B, 3909)
+    announce(f"attention query hf B=1 S={s} causal")
+    out = _run(xs.to(gpu), True, norm_style="hf")
+    rows = torch.unique(torch.cat([torch.arange(0, 4), torch.arange(0, s, 97), torch.arange(s - 4, s)]))
+    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
+    m = oracle.metric(out[:, :, rows], ref)
+    assert m["pass"], m
+
+
 @pytest.mark.parametrize("s", [33, 129])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("mode", ["query", "unfused"])

@@ -99,6 +99,28 @@ def test_prepare_only_k_leaves_q(gpu):
     assert oracle.norm_rope_gate(kn.cpu(), ref)["pass"]
 
 
+@pytest.mark.parametrize("b,s", [(1, 512), (1, 2048)])
+@pytest.mark.parametrize("style", ["fp32", "hf"])
+def test_sweep_small_shapes_whole_tensor(gpu, b, s, style):
+    """The two smaller bandwidth-sweep shapes (config 2), every element: the
+    FP32 style passes the norm+RoPE gate against the FP32 oracle; the HF
+    style passes the reference metric against it and equals the oracle's
+    restated HF chain to one ulp on a vanishing fraction of elements."""
+    xs = make_inputs(b, s, QWEN3_8B, 1909)
+    announce(f"norm_rope {style} sweep shape B={b} S={s}")
+    qn, kn = norm_rope(*[t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin)], norm_style=style)
+    torch.cuda.synchronize()
+    rq, rk = _oracle_fp32(xs)
+    for got, ref in ((qn, rq), (kn, rk)):
+        m = (oracle.norm_rope_gate if style == "fp32" else oracle.metric)(got.cpu(), ref)
+        assert m["pass"], m
+    if style == "hf":
+        for got, (ref, scale) in zip((qn.cpu(), kn.cpu()), _oracle_chain(xs, style)):
+            diff = (got.float() - ref.float()).abs()
+            assert bool((diff <= bf16_ulp(scale) + bf16_ulp(ref)).all())
+            assert float((diff > 0).float().mean()) < 2e-3
+
+
 @pytest.mark.parametrize("b,s", [(1, 8192), (4, 2048), (8, 1024), (16, 512)])
 def test_full_size_row_sample(gpu, b, s):
     """Bandwidth-sweep shapes: every launch covers all rows; a row sample is

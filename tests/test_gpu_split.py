@@ -110,3 +110,45 @@ def test_split_cached_workspace_per_stream(gpu):
     torch.cuda.synchronize()
     for out in outs:
         assert torch.equal(out, ref)
+
+
+def test_captured_split_keeps_its_workspace(gpu):
+    """A launch captured with work=None gets a workspace of its own from the
+    graph's memory pool, also when the capture comes before any eager launch
+    on that stream (it still splits: its output equals the eager split
+    output bit for bit, which differs from the unsplit one).  Growing the
+    eager cache afterwards (a larger split shape on the same stream) must not
+    disturb replays, which are compared bit for bit with eager results."""
+    small = make_inputs(1, 2048, (8, 4, 256), 1717).to(gpu)
+    large = make_inputs(1, 2048, (16, 8, 256), 1818).to(gpu)
+    kn_s, kn_l = torch.empty_like(small.k), torch.empty_like(large.k)
+    prepare_attention(small.reference7, None, kn_s, only_k=True, norm_style="fp32")
+    prepare_attention(large.reference7, None, kn_l, only_k=True, norm_style="fp32")
+    torch.cuda.synchronize()
+    out = torch.empty_like(small.q)
+    fn = lambda: attention_prefill(small.q, kn_s, small.v, out, gq=small.gq, cos=small.cos, sin=small.sin,
+                                   causal=True, norm_style="fp32")
+    announce("split capture before eager use, then cache growth")
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            fn()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    unsplit = _run(small, kn_s, True, torch.empty(0, dtype=torch.uint8, device=gpu))
+    split = _run(small, kn_s, True, None)
+    torch.cuda.synchronize()
+    assert not torch.equal(split, unsplit), "shape expected to split"
+    for i in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, split), i
+        big = _run(large, kn_l, True, None)  # grows this stream's cached workspace
+        again = _run(small, kn_s, True, None)
+        torch.cuda.synchronize()
+        assert torch.equal(again, split), i
+    ref = oracle.oracle_rows_fp32(*[t.cpu() for t in large.astuple()], torch.arange(2040, 2048), True)
+    assert oracle.attention_gate(big[:, :, 2040:].cpu(), ref)["pass"]
