@@ -129,6 +129,27 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
                                int norm_style, int bm, int bn, void *work, int64_t work_bytes,
                                void *stream);
 
+/* kfmi_launch_attention_bf16 without the work/work_bytes arguments, for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference,
+ * whose launches never split a query block and so need no workspace.  The
+ * split-KV workspace of the causal D = 256 shapes that split (see
+ * kfmi_attention_workspace_bytes) is a static device array of 36 MiB per GPU
+ * (held by each GPU the library runs on until the process ends); a shape
+ * whose split plan needs more returns KFMI_EINVAL before anything is
+ * launched.  The call allocates nothing: when the shape splits it enqueues a
+ * small fill kernel that zeroes the plan's arrival counters ahead of the
+ * other launches.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap in time on one GPU (several streams, or concurrent graph
+ * replays) race on it.  Results are identical to kfmi_launch_attention_bf16
+ * with a zero-filled caller workspace. */
+int kfmi_launch_attention_bf16_noalloc(const void *q, const void *k, const void *v,
+                                       const void *gq, const void *gk, const void *cos,
+                                       const void *sin, void *out, void *qn, void *kn, void *vt,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D,
+                                       double scale, float eps, int causal, int mode,
+                                       int norm_style, int bm, int bn, void *stream);
+
 /* vt[b,h,d,s] = v[b,h,s,d] for B*H heads of S rows of D (D 128 or 256,
  * S % 8 == 0): the V^T scratch of kfmi_launch_attention_bf16, as a separate
  * launch.  No counterpart in the reference (its kernels read V directly). */

@@ -35,6 +35,8 @@ SIGNATURES = {
     "kfmi_transpose_v_bf16": [_P, _P, _I64, _I64, _I64, _P],
     "kfmi_launch_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _D,
                                    _F, _I, _I, _I, _I, _I, _P, _I64, _P],
+    "kfmi_launch_attention_bf16_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                                           _D, _F, _I, _I, _I, _I, _I, _P],
     "kfmi_factored_prepare_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
     "kfmi_factored_attention_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P],
     "kfmi_launch_factored_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I,

@@ -1372,6 +1372,13 @@ int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
   return split_counter_bytes(pairs) + split_partial_bytes(pairs, D);
 }
 
+int64_t attention_workspace_counter_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal) {
+  if (attention_uses_pp(Hq, Hkv, S, D)) return 0;
+  SplitPlan pl;
+  if (!plan_split(B, Hq, S, D, causal, device_cus(), pl)) return 0;
+  return split_counter_bytes((int64_t)pl.n_split * B * Hq);
+}
+
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   constexpr double LOG2E = 1.4426950408889634;
   AttnParams p;

@@ -176,11 +176,14 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
                         style_of(norm_style), bm, bn, (hipStream_t)stream, work, work_bytes);
 }
 
-int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
-                               const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt, int64_t B,
-                               int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal,
-                               int mode, int norm_style, int bm, int bn, void *work, int64_t work_bytes,
-                               void *stream) {
+// Shared body of kfmi_launch_attention_bf16 and its allocation-free variant
+// (noalloc: the split-KV workspace is the static per-GPU scratch array
+// instead of the caller's `work`).
+static int launch_attention_entry(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                                  const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt,
+                                  int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps,
+                                  int causal, int mode, int norm_style, int bm, int bn, void *work,
+                                  int64_t work_bytes, void *stream, bool noalloc) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_style(norm_style));
   KFMI_TRY(check_tiles(bm, bn));
@@ -188,23 +191,43 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
     return fail(KFMI_EINVAL, "Invalid fusion mode %d", mode);
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}}));
   KFMI_TRY(check_work(work, work_bytes));
-  if (mode == KFMI_MODE_FULL) {  // one launch, K normalised per tile; no scratch (rope:671-677)
-    if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
-    if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
-    if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
-    KFMI_TRY(check_device());
-    return attention_impl(q, k, v, nullptr, gq, gk, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal,
-                          cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM, style_of(norm_style), bm, bn,
-                          (hipStream_t)stream, work, work_bytes);
+  if (mode != KFMI_MODE_FULL) {
+    if (kn == nullptr || (mode == KFMI_MODE_UNFUSED && qn == nullptr)) return fail(KFMI_EINVAL, "Missing scratch buffers");
+    KFMI_TRY(check_ptrs({{kn, "kn"}}));
+    if (mode == KFMI_MODE_UNFUSED) KFMI_TRY(check_ptrs({{qn, "qn"}}));
+    if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
   }
-  if (kn == nullptr || (mode == KFMI_MODE_UNFUSED && qn == nullptr)) return fail(KFMI_EINVAL, "Missing scratch buffers");
-  KFMI_TRY(check_ptrs({{kn, "kn"}}));
-  if (mode == KFMI_MODE_UNFUSED) KFMI_TRY(check_ptrs({{qn, "qn"}}));
   if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
   if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
-  if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_device());
+  int64_t clear_bytes = 0;
+  if (noalloc) {
+    const int64_t need = kfmi::attention_workspace_bytes(B, Hq, Hkv, S, D, causal != 0);
+    if (need > KFMI_SCRATCH_BYTES)
+      return fail(KFMI_EINVAL,
+                  "split-KV workspace of %lld bytes exceeds the static scratch of %lld bytes "
+                  "(use kfmi_launch_attention_bf16 with a caller workspace for this shape)",
+                  (long long)need, (long long)KFMI_SCRATCH_BYTES);
+    work = nullptr;
+    work_bytes = 0;
+    if (need > 0) {
+      hipError_t e = kfmi::noalloc_scratch(&work);
+      if (e != hipSuccess) return launch_status(e, "static scratch address");
+      work_bytes = KFMI_SCRATCH_BYTES;
+      clear_bytes = kfmi::attention_workspace_counter_bytes(B, Hq, Hkv, S, D, causal != 0);
+    }
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (clear_bytes > 0) {  // the arrival counters start each launch at zero
+    hipError_t e = kfmi::clear_scratch_words(work, clear_bytes, st);
+    if (e != hipSuccess) return launch_status(e, "scratch clear launch");
+  }
+  if (mode == KFMI_MODE_FULL) {  // one launch, K normalised per tile; no scratch (rope:671-677)
+    return attention_impl(q, k, v, nullptr, gq, gk, cos, sin, out, nullptr, B, Hq, Hkv, S, D, scale, eps, causal,
+                          cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM, style_of(norm_style), bm, bn, st, work,
+                          work_bytes);
+  }
   const bool rope = cos != nullptr;
   // V^T is used by the ping-pong kernel when its rows are 16-byte aligned.
   const bool use_vt = vt != nullptr && kfmi::attention_uses_pp(Hq, Hkv, S, D) && S % 8 == 0;
@@ -217,12 +240,30 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, cons
     r.v = (const uint16_t *)v;
     r.vt = (uint16_t *)vt;
   }
-  hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
+  hipError_t e = kfmi::launch_rows(r, st);
   if (e != hipSuccess) return launch_status(e, "prepare launch");
   const bool query = mode == KFMI_MODE_QUERY;
   const int pro = !query ? kfmi::PRO_NONE : (rope ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   return attention_impl(query ? q : qn, kn, v, use_vt ? vt : nullptr, gq, nullptr, cos, sin, out, nullptr, B, Hq, Hkv, S, D,
-                        scale, eps, causal, pro, style_of(norm_style), bm, bn, (hipStream_t)stream, work, work_bytes);
+                        scale, eps, causal, pro, style_of(norm_style), bm, bn, st, work, work_bytes);
+}
+
+int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                               const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale, float eps, int causal,
+                               int mode, int norm_style, int bm, int bn, void *work, int64_t work_bytes,
+                               void *stream) {
+  return launch_attention_entry(q, k, v, gq, gk, cos, sin, out, qn, kn, vt, B, Hq, Hkv, S, D, scale, eps, causal,
+                                mode, norm_style, bm, bn, work, work_bytes, stream, false);
+}
+
+int kfmi_launch_attention_bf16_noalloc(const void *q, const void *k, const void *v, const void *gq, const void *gk,
+                                       const void *cos, const void *sin, void *out, void *qn, void *kn, void *vt,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, double scale,
+                                       float eps, int causal, int mode, int norm_style, int bm, int bn,
+                                       void *stream) {
+  return launch_attention_entry(q, k, v, gq, gk, cos, sin, out, qn, kn, vt, B, Hq, Hkv, S, D, scale, eps, causal,
+                                mode, norm_style, bm, bn, nullptr, 0, stream, true);
 }
 
 int kfmi_transpose_v_bf16(const void *v, void *vt, int64_t BH, int64_t S, int64_t D, void *stream) {

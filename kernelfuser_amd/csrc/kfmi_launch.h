@@ -62,5 +62,20 @@ bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D);
 // Workspace bytes with which launch_attention splits the key range of the
 // longest causal query blocks over two workgroups (0: this shape never splits).
 int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal);
+// Leading bytes of that workspace that hold the arrival counters, which must
+// be zero when a launch starts (0: this shape never splits).
+int64_t attention_workspace_counter_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal);
+
+// Static split-KV workspace of the allocation-free entry point (one per GPU):
+// 36 MiB covers every causal D = 256 split plan of up to 141 (block, head)
+// pairs, which includes the Gemma-3 geometries up to their largest
+// one-workgroup-per-CU grids (at most 128 pairs, 32.5 MiB).
+#define KFMI_SCRATCH_BYTES (36ll << 20)
+// Device address of the current device's static workspace (taken once per
+// device with hipGetSymbolAddress and cached).
+hipError_t noalloc_scratch(void **addr);
+// Zero the first `bytes` (a multiple of 4) of the static workspace on `stream`
+// with a fill kernel.
+hipError_t clear_scratch_words(void *addr, int64_t bytes, hipStream_t stream);
 
 }  // namespace kfmi
