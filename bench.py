@@ -49,8 +49,11 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100, help="timed steps of the headline workload")
-    ap.add_argument("--warmup", type=int, default=300,
-                    help="untimed steps first; the GPU clock needs tens of ms of load to settle")
+    ap.add_argument("--warmup", type=int, default=300, help="untimed steps first")
+    ap.add_argument("--settle-ms", type=float, default=400.0,
+                    help="after the warmup steps, further untimed steps until this much wall time of "
+                         "continuous load has passed: the GPU clock needs a few hundred ms of load to settle, "
+                         "whatever --warmup is")
     ap.add_argument("--seq", type=int, default=4096, help="headline sequence length")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--norm-style", default="fp32", choices=["fp32", "hf", "legacy"])
@@ -72,36 +75,11 @@ def _events():
 
 
 def time_graph(fn, n, replays=10):
-    """Average device time (ms) per call of ``fn(i)``, i = 0..n-1, captured
-    into one HIP graph (torch.cuda.CUDAGraph) and replayed ``replays`` times
-    after warmup replays: the launch-rate-independent timing of the
-    reference's harness (src/fusion_harness.py:32-79).  Median over replays."""
-    import torch
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for i in range(min(n, 3)):
-            fn(i)
-        stream.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(n):
-                fn(i)
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    for _ in range(3):
-        graph.replay()
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(replays):
-        a, b = _events()
-        a.record()
-        graph.replay()
-        b.record()
-        b.synchronize()
-        times.append(a.elapsed_time(b) / n)
-    del graph
-    return statistics.median(times)
+    """Average device time (ms) per call of ``fn(i)``, i = 0..n-1, as one HIP
+    graph block replayed ``replays`` times (median), with the package's paced
+    timing protocol (kernelfuser_amd.timing)."""
+    from kernelfuser_amd import timing
+    return timing.block_time_us(fn, n, replays=replays) * 1e-3
 
 
 def load_traffic():
@@ -124,8 +102,15 @@ def headline(args, torch, kf):
     kn = torch.empty_like(xs.k)
     step = lambda: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn,
                                        norm_style=args.norm_style)
+    t_settle = time.perf_counter()
     for _ in range(args.warmup):
         step()
+    settle_steps = 0
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(20):
+            step()
+        settle_steps += 20
+        torch.cuda.synchronize()
     torch.cuda.synchronize()
     ev0, ev1 = _events()
     t0 = time.perf_counter()
@@ -139,7 +124,7 @@ def headline(args, torch, kf):
     flops = kf.attention_flops(b, hq, s, d, True)
     ms_step = wall_ms / args.steps
     res = {"flops_per_step": flops, "ms_per_step": ms_step, "device_ms_per_step": dev_ms / args.steps,
-           "tflops": flops / (ms_step * 1e-3) / 1e12}
+           "tflops": flops / (ms_step * 1e-3) / 1e12, "settle_steps": settle_steps}
     # The two kernels separately (events on the launch stream).
     attn_ms = time_graph(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
                                                            causal=True, fuse_q=True, norm_style=args.norm_style),
@@ -218,7 +203,8 @@ def cpu_baseline(args, torch, xs_cpu, out_gpu):
     sample of the headline workload: KV group 0 (Q heads 0-3, KV head 0) of
     B=1, S=seq.  Also checks the GPU output on that sample (attention gate)."""
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host_cpus = os.cpu_count() or 1
+    threads = max(1, min(16, host_cpus))  # the box's CPU share is 16 threads
     torch.set_num_threads(threads)
     hq, hkv, d = QWEN3_8B
     g = hq // hkv
@@ -229,15 +215,15 @@ def cpu_baseline(args, torch, xs_cpu, out_gpu):
         t0 = time.perf_counter()
         ref = oracle.oracle_fp32(q, k, v, xs_cpu.gq, xs_cpu.gk, xs_cpu.cos, xs_cpu.sin, True)
         times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
     f = 4 * q.shape[0] * g * d * (q.shape[2] * (q.shape[2] + 1) // 2)
     med = statistics.median(times[1:] if len(times) > 2 else times)
     gate = oracle.attention_gate(out_gpu[:, :g].float().cpu(), ref)
-    res = {"value": f / med / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    res = {"value": f / med / 1e12, "unit": "TFLOP/s", "cores": threads, "host_cpus": host_cpus, "kind": "port",
+           "sample_share_of_workload": g / hq,
            "sample": (f"oracle_fp32 (eager FP32 torch: RMSNorm, RoPE, SDPA) on KV group 0 of the headline "
-                      f"workload: B=1, Hq=4, Hkv=1, S={q.shape[2]}, D=128, causal; {len(times)} calls in "
-                      f"{sum(times):.1f} s, median {med * 1e3:.1f} ms"),
+                      f"workload (1/{hkv} of its FLOPs): B=1, Hq={g}, Hkv=1, S={q.shape[2]}, D=128, causal; "
+                      f"{len(times)} calls in {sum(times):.1f} s, median {med * 1e3:.1f} ms; rate = that "
+                      f"sample's FLOPs / its median time, on {threads} threads"),
            "parity": {k2: gate[k2] for k2 in ("max_abs", "mean_abs", "relative_l2", "pass")}}
     # norm+RoPE CPU leg on the largest sweep shape, in GB/s.
     nr = None
@@ -252,11 +238,9 @@ def cpu_baseline(args, torch, xs_cpu, out_gpu):
             oracle.norm_rope_fp32(xs.q, xs.gq, xs.cos, xs.sin).to(torch.bfloat16)
             oracle.norm_rope_fp32(xs.k, xs.gk, xs.cos, xs.sin).to(torch.bfloat16)
             nt.append(time.perf_counter() - t0)
-            if len(nt) >= 50:
-                break
         m = statistics.median(nt[1:] if len(nt) > 2 else nt)
         by = 4 * 8192 * 40 * 128 + 2 * 8192 * 128 + 4 * 128
-        nr = {"value": by / m / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+        nr = {"value": by / m / 1e9, "unit": "GB/s", "cores": threads, "host_cpus": host_cpus, "kind": "port",
               "sample": f"norm_rope_fp32 of Q and K at B=1, S=8192 (Qwen3-8B heads), {len(nt)} calls, "
                         f"median {m * 1e3:.1f} ms"}
     finally:
@@ -329,11 +313,16 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "attn_pp_kernel (fused Q norm+RoPE prologue, ping-pong waves)",
                      "achieved": head["attention_kernel_tflops"], "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                      "frac": head["attention_kernel_tflops"] / MFMA_BF16_PEAK_TFS,
-                     "kernel_us": head["attention_kernel_us"], "traffic": traffic},
+                     "kernel_us": head["attention_kernel_us"], "traffic": traffic,
+                     "frac_step_device": head["flops_per_step"] / (head["device_ms_per_step"] * 1e-3) / 1e12
+                     / MFMA_BF16_PEAK_TFS,
+                     "frac_step_wall": head["tflops"] / MFMA_BF16_PEAK_TFS,
+                     "frac_note": "frac: attention kernel alone (graph-replay events); frac_step_*: the whole "
+                                  "step (K-prep launch + attention) by device events / by the host clock"},
         "kernels": {"attention_us": head["attention_kernel_us"],
                     "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
                     "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows (one launch)",
-                    "device_ms_per_step": head["device_ms_per_step"]},
+                    "device_ms_per_step": head["device_ms_per_step"], "settle_steps": head["settle_steps"]},
     }
     if not args.quick:
         line["norm_rope"] = norm_rope_sweep(args, torch, kf)

@@ -76,5 +76,52 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     return LIB
 
 
+def resources() -> list[dict]:
+    """Per-kernel resource usage of every template instance in ``csrc/``, from
+    the compiler's own report (``-Rpass-analysis=kernel-resource-usage``, the
+    same flags as the build, device pass only): VGPRs, AGPRs, SGPRs, spills,
+    scratch, LDS and waves per SIMD."""
+    import re
+    cc = hipcc()
+    rows: list[dict] = []
+    for src in sorted(CSRC.glob("*.hip")):
+        cmd = [cc, *COMMON, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "--cuda-device-only", "-c", str(src),
+               "-o", os.devnull, "-Rpass-analysis=kernel-resource-usage"]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"resource report failed for {src.name}:\n{res.stderr[-2000:]}")
+        cur = None
+        for line in res.stderr.splitlines():
+            m = re.search(r"remark: Function Name: (\S+)", line)
+            if m:
+                cur = {"file": src.name, "symbol": m.group(1)}
+                rows.append(cur)
+                continue
+            m = re.search(r"remark:\s+([A-Za-z][A-Za-z /\[\]]*?):\s+(\S+) \[-Rpass", line)
+            if m and cur is not None:
+                cur[m.group(1).strip()] = m.group(2)
+    filt = shutil.which("llvm-cxxfilt") or shutil.which("c++filt")
+    if filt and rows:
+        out = subprocess.run([filt], input="\n".join(r["symbol"] for r in rows), capture_output=True, text=True)
+        for r, name in zip(rows, out.stdout.splitlines()):
+            r["name"] = name.replace("kfmi::(anonymous namespace)::", "").replace("(kfmi::(anonymous namespace)::", "(")
+    return rows
+
+
+def resources_markdown(rows: list[dict]) -> str:
+    cols = [("VGPRs", "VGPRs"), ("AGPRs", "AGPRs"), ("TotalSGPRs", "SGPRs"), ("VGPRs Spill", "VGPR spill"),
+            ("SGPRs Spill", "SGPR spill"), ("ScratchSize [bytes/lane]", "scratch B/lane"),
+            ("LDS Size [bytes/block]", "LDS B/block"), ("Occupancy [waves/SIMD]", "waves/SIMD")]
+    lines = ["| file | kernel instance | " + " | ".join(c[1] for c in cols) + " |",
+             "|" + "---|" * (2 + len(cols))]
+    for r in rows:
+        lines.append(f"| {r['file']} | `{r.get('name', r['symbol'])}` | "
+                     + " | ".join(str(r.get(c[0], "")) for c in cols) + " |")
+    return "\n".join(lines) + "\n"
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--resources" in sys.argv:
+        print(resources_markdown(resources()), end="")
+    else:
+        print(build(verbose="-v" in sys.argv))

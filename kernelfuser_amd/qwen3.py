@@ -33,8 +33,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import random
-import statistics
 import time
 import types
 from pathlib import Path
@@ -164,8 +162,12 @@ def forward_logits(model, ids):
         return model(input_ids=ids, attention_mask=None, use_cache=False, return_dict=True).logits
 
 
-def _nll(logits, ids):
-    return F.cross_entropy(logits[:, :-1, :].float().reshape(-1, logits.shape[-1]), ids[:, 1:].reshape(-1))
+def next_token_nll(logits, ids) -> float:
+    """Mean negative log-likelihood of ids[:, t+1] under logits[:, t] (FP32
+    log-softmax; the last position has no target)."""
+    logp = torch.log_softmax(logits[:, :-1].float(), dim=-1)
+    picked = torch.gather(logp, -1, ids[:, 1:, None]).squeeze(-1)
+    return float(-picked.mean())
 
 
 def quality(candidate: torch.Tensor, reference: torch.Tensor, ids: torch.Tensor) -> dict:
@@ -173,7 +175,7 @@ def quality(candidate: torch.Tensor, reference: torch.Tensor, ids: torch.Tensor)
     c, r = candidate.float(), reference.float()
     d = c - r
     top = float((c.argmax(-1) == r.argmax(-1)).float().mean())
-    nll_r, nll_c = float(_nll(reference, ids)), float(_nll(candidate, ids))
+    nll_r, nll_c = next_token_nll(reference, ids), next_token_nll(candidate, ids)
     m = {"max_abs": float(d.abs().max()), "relative_l2": float(d.norm() / r.norm().clamp_min(1e-12)),
          "allclose": bool(torch.allclose(c, r, atol=ATOL, rtol=RTOL)), "top1_agreement": top,
          "nll_reference": nll_r, "nll_candidate": nll_c, "nll_abs_diff": abs(nll_c - nll_r)}
@@ -181,44 +183,40 @@ def quality(candidate: torch.Tensor, reference: torch.Tensor, ids: torch.Tensor)
     return m
 
 
-def _capture(fn, warmup):
-    with torch.inference_mode():
-        for _ in range(max(3, warmup)):
-            fn()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            static = fn()
-        graph.replay()
-        torch.cuda.synchronize()
-    return graph, static
+def _forward_with(model, ids, arm: str):
+    """Logits with every attention layer switched to ``arm`` for this call
+    only (the patch is Python-level, so a graph captured from this call
+    records that arm's kernels)."""
+    saved = patch(model, arm)
+    try:
+        return forward_logits(model, ids)
+    finally:
+        restore(saved)
 
 
-def _timed_pair(base, cand, repeats, rounds, seed):
-    """Randomized paired graph replays (e2:185-213)."""
-    rng = random.Random(seed)
-    bv, cv, order = [], [], []
+def timed_arms(model, ids, eager_candidate, *, rounds: int, samples: int, seed: int) -> dict:
+    """Reference and candidate prefill timed with ``timing.interleaved`` (one
+    forward per graph block, fresh captures per round); each replayed
+    candidate output must stay within 1e-3 relative L2 of the eager one."""
+    from . import timing
 
-    def measure(g):
-        a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        g.replay()
-        z.record()
-        z.synchronize()
-        return float(a.elapsed_time(z))
+    def check(name, out):
+        if name == "candidate":
+            rel = float((out.float() - eager_candidate.float()).norm() / eager_candidate.float().norm())
+            if not rel <= 1e-3:
+                raise RuntimeError(f"replayed candidate logits drifted from the eager call: rel-L2 {rel}")
 
-    for _ in range(rounds * repeats):
-        if rng.random() < 0.5:
-            order.append("reference,candidate")
-            bv.append(measure(base))
-            cv.append(measure(cand))
-        else:
-            order.append("candidate,reference")
-            cv.append(measure(cand))
-            bv.append(measure(base))
-    return {"reference_ms": bv, "candidate_ms": cv, "arm_order": order, "seed": seed,
-            "reference_median_ms": statistics.median(bv), "candidate_median_ms": statistics.median(cv),
-            "speedup": statistics.median(bv) / statistics.median(cv), "repeats": repeats, "rounds": rounds}
+    arms = {"reference": lambda: _forward_with(model, ids, "reference"),
+            "candidate": lambda: _forward_with(model, ids, "fused")}
+    res = timing.interleaved(arms, rounds=rounds, samples=samples, launches=1, seed=seed, baseline="candidate",
+                             check=check)
+    ref, cand = res["arms"]["reference"], res["arms"]["candidate"]
+    return {"reference_median_us": ref["median_us"], "candidate_median_us": cand["median_us"],
+            "reference_p10_p90_us": [ref["p10_us"], ref["p90_us"]],
+            "candidate_p10_p90_us": [cand["p10_us"], cand["p90_us"]],
+            "speedup_paired_median": res["paired_ratio"]["reference"]["median"],
+            "speedup_ci95": res["paired_ratio"]["reference"]["ci95"],
+            "protocol": {k: v for k, v in res["protocol"].items() if k != "orders"}}
 
 
 def noise_floor_gate(candidate: dict, floor: dict) -> bool:
@@ -234,7 +232,7 @@ def noise_floor_gate(candidate: dict, floor: dict) -> bool:
                 and candidate["nll_abs_diff"] <= NLL_ATOL)
 
 
-def run_row(model, b: int, s: int, *, warmup: int = 5, repeats: int = 10, rounds: int = 3, timing: bool = True):
+def run_row(model, b: int, s: int, *, samples: int = 10, rounds: int = 3, timing: bool = True):
     """One (B, S) row: correctness gates first, then paired graph timing.
 
     status 'pass': the reference's gates hold; 'pass_noise_floor': they do not,
@@ -247,7 +245,6 @@ def run_row(model, b: int, s: int, *, warmup: int = 5, repeats: int = 10, rounds
     saved = patch(model, "reference")
     try:
         ref = forward_logits(model, ids)
-        gb = _capture(lambda: forward_logits(model, ids), warmup)[0] if timing else None
     finally:
         restore(saved)
     saved = patch(model, "floor")
@@ -267,11 +264,10 @@ def run_row(model, b: int, s: int, *, warmup: int = 5, repeats: int = 10, rounds
         else:
             row["status"] = "fail_candidate_correctness"
             return row
-        if timing:
-            gc = _capture(lambda: forward_logits(model, ids), warmup)[0]
-            row["timing"] = _timed_pair(gb, gc, repeats, rounds, seed)
     finally:
         restore(saved)
+    if timing:
+        row["timing"] = timed_arms(model, ids, got, rounds=rounds, samples=samples, seed=seed)
     return row
 
 
@@ -283,8 +279,7 @@ def main(argv=None):
     ap.add_argument("--out", required=True)
     ap.add_argument("--sizes", nargs="+", type=int, default=[128, 256])
     ap.add_argument("--batches", nargs="+", type=int, default=[1, 8, 32])
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--repeats", type=int, default=20)
+    ap.add_argument("--samples", type=int, default=20)
     ap.add_argument("--rounds", type=int, default=5)
     args = ap.parse_args(argv)
     model = load_qwen3(args.model) if args.model else random_qwen3(args.random_layers)
@@ -297,12 +292,13 @@ def main(argv=None):
     out.parent.mkdir(parents=True, exist_ok=True)
     for b in args.batches:
         for s in args.sizes:
-            row = run_row(model, b, s, warmup=args.warmup, repeats=args.repeats, rounds=args.rounds)
+            row = run_row(model, b, s, samples=args.samples, rounds=args.rounds)
             rec["rows"].append(row)
             out.write_text(json.dumps(rec, indent=1) + "\n")
             t = row.get("timing", {})
             print(f"B={b} S={s} {row['status']} max_abs={row['correctness']['max_abs']:.4f} "
-                  f"top1={row['correctness']['top1_agreement']:.4f} speedup={t.get('speedup', float('nan')):.3f}",
+                  f"top1={row['correctness']['top1_agreement']:.4f} "
+                  f"speedup={t.get('speedup_paired_median', float('nan')):.3f}",
                   flush=True)
     return rec
 

@@ -1,0 +1,34 @@
+"""Refinement runner end to end on the GPU (one short row of each kind): every
+arm of this package passes the reference gate, the selection and the retest
+run, extra seeds pass, and the tail checks pass for every mode."""
+import pytest
+
+from helpers import announce
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("model,b,s,causal,rotary", [("Qwen3-8B", 1, 128, True, True),
+                                                     ("Gemma-3-4B", 1, 256, False, False)])
+def test_refine_row(gpu, model, b, s, causal, rotary):
+    from kernelfuser_amd import refine
+    announce(f"refine row {model} B={b} S={s} causal={causal} rope={rotary}")
+    row = refine.run_row(model, b, s, causal, rotary, rounds=(1, 1), samples=(2, 3), launches=5)
+    assert row["status"] == "passed", row.get("correctness")
+    for name in ("query", "full", "unfused") + (() if rotary else ("factored",)):
+        assert row["correctness"][name]["pass"], (name, row["correctness"][name])
+    sm = row["summary"]
+    assert sm["fused_us"] > 0 and sm["unfused_us"] > 0 and sm["retest_speedup"] > 0
+    assert row["selected_fused"] in ("query", "full", "factored")
+    assert len(row["additional_seed_checks"]) == 4
+    v = row["correctness"]["vendor_unfused"]
+    assert v["pass"] or "error" in v  # unavailable on this PyTorch build is recorded, not hidden
+
+
+def test_refine_tails(gpu):
+    from kernelfuser_amd import refine
+    announce("refine tail checks S=33/129")
+    recs = refine.tail_checks()
+    assert len(recs) == 2 * 2 * 2 * 3 + 2 * 2 * 1  # Gemma rows add the factored arm
+    bad = [r for r in recs if not r["pass"]]
+    assert not bad, bad
