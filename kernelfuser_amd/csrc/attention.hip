@@ -159,6 +159,10 @@ __device__ __forceinline__ void copy16_to_lds(const i32x4_t &rsrc, uint32_t lds,
 __device__ __forceinline__ void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 constexpr float RESCALE_SLACK = 8.0f;  // log2 units: probabilities stay <= 2^8
+// Lean-softmax guard: a lane's partial sum of one tile's probabilities must
+// stay below 2^64, so every probability does and O accumulates far inside
+// FP32 range; otherwise the work item is redone with the exact softmax.
+constexpr float FAST_LIMIT = 0x1p64f;
 
 // Phase fences: an empty volatile asm that takes the phase's results as
 // inputs, so the compiler finishes computing them before the barrier that
@@ -377,7 +381,7 @@ struct Softmax {
   static constexpr int NKB = BN / 32, NK16 = BN / 16, NDB = D / 32;
   float m_run = FOLD ? 0.f : -INFINITY;  // reference max of logits (log2 domain)
   float l_run = 0.f;                     // this lane's partial row sum
-  bool started = false;                  // FOLD: a tile has set m_run
+  bool started = false;                  // a tile has set m_run (FOLD and step_lean)
 
   // GEMM1 accumulator start value of this lane (FOLD: -m_run).
   __device__ __forceinline__ float acc_init() const { return FOLD ? -m_run : 0.f; }
@@ -462,8 +466,74 @@ struct Softmax {
         }
     }
     l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-    // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
-    // (registers 4q..4q+3 of a block hold keys 8q + 4*g + 0..3).
+    pack(s, pb);
+  }
+
+  // Lean tile (the general kernel's hot path).  The first tile of a sweep
+  // (FIRST, peeled by the caller so later tiles carry no branch) sets m_run
+  // to the tile's exact row max (O and l are still zero, so nothing is
+  // rescaled); every later tile takes p = exp2(logit - m_run)
+  // with no max reduction and no rescale.  That is the same softmax (one
+  // constant shift per row), valid as long as no probability overflows:
+  // a lane whose partial tile sum is not below FAST_LIMIT sets `bad` (rows
+  // at or past S excluded), and the caller then redoes the whole work item
+  // with step().  O never changes here, which keeps this path's register
+  // footprint at that of the accumulators alone.
+  template <bool FIRST>
+  __device__ __forceinline__ void step_lean(f32x16_t (&s)[NKB], int t, int q0, int qrow, int64_t S, int g, float cl,
+                                            bf16x8_t (&pb)[NK16], bool &bad) {
+    const int kt = t * BN;
+    const bool need_mask = (CAUSAL && kt + BN - 1 > q0) || (kt + BN > S);
+    if (need_mask) {
+      const int last = (int)(S - 1);
+      const int lim = (CAUSAL ? (qrow < last ? qrow : last) : last) - kt - 4 * g;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (32 * kb + 8 * (i >> 2) + (i & 3) > lim) s[kb][i] = -INFINITY;
+    }
+    if constexpr (FIRST) {
+      float mt[NKB * 8];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mt[kb * 8 + i] = fmaxf(s[kb][2 * i], s[kb][2 * i + 1]);
+#pragma unroll
+      for (int n = NKB * 8; n > 1; n = (n + 1) / 2)
+#pragma unroll
+        for (int i = 0; i + (n + 1) / 2 < n; ++i) mt[i] = fmaxf(mt[i], mt[i + (n + 1) / 2]);
+      const float mx = max_halves(mt[0]);
+      if constexpr (FOLD) {
+        m_run += mx;  // scores held logit - m_run with m_run = 0
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[kb][i] -= mx;
+      } else {
+        m_run = mx * cl;
+      }
+      started = true;
+    }
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+    const float nm = -m_run;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float pv = FOLD ? __builtin_amdgcn_exp2f(s[kb][i]) : __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][i], cl, nm));
+        s[kb][i] = pv;
+        ls[i & 3] += pv;
+      }
+    const float lt = (ls[0] + ls[1]) + (ls[2] + ls[3]);
+    l_run += lt;
+    bad |= qrow < S && !(lt < FAST_LIMIT);
+    pack(s, pb);
+  }
+
+  // P^T operands: 16-key step c2 <- registers 8*(c2%2) .. +7 of block c2/2
+  // (registers 4q..4q+3 of a block hold keys 8q + 4*g + 0..3).
+  __device__ __forceinline__ void pack(const f32x16_t (&s)[NKB], bf16x8_t (&pb)[NK16]) const {
 #pragma unroll
     for (int c2 = 0; c2 < NK16; ++c2) {
       u32x4_t wv;
@@ -487,6 +557,7 @@ struct Softmax {
 };
 
 // GEMM1: S^T (BN keys x 32 queries) of the K tile at LDS byte kbuf.
+constexpr int G1_AHEAD = 2;
 template <int D, int BN>
 __device__ __forceinline__ void gemm1(const unsigned char *smem, int kbuf, const uint32_t (&kra)[8],
                                       const bf16x8_t (&qreg)[D / 16], f32x16_t (&s)[BN / 32]) {
@@ -501,12 +572,14 @@ __device__ __forceinline__ void gemm1(const unsigned char *smem, int kbuf, const
       s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[c], s[kb], 0, 0, 0);
     }
   }
-  // Issue order: K reads run two MFMAs ahead (bounded register footprint).
-  __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  // Issue order: K reads run G1_AHEAD MFMAs ahead, so an MFMA's operand was
+  // requested several MFMAs (~32 cycles each) before it, past the LDS
+  // latency.
+  __builtin_amdgcn_sched_group_barrier(0x100, G1_AHEAD, 0);
 #pragma unroll
   for (int i = 0; i < NKB * NC; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (i + 2 < NKB * NC) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if (i + G1_AHEAD < NKB * NC) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
   }
 }
 
@@ -1119,15 +1192,17 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   }
 
   f32x16_t o[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
   Softmax<D, BN, CAUSAL> sm;
+  bool bad = false;  // a lean tile of this lane failed its overflow guard
 
   // Pipeline (one barrier per KV tile): iteration t issues the copies of
   // K(t+2) and V(t+1), then GEMM1 of tile t+1 and the softmax + GEMM2 of tile
-  // t; each copy has a full iteration to land.  PAR = t % 2 selects buffers.
-  auto iteration = [&](auto par, int t, f32x16_t (&cur)[NKB], f32x16_t (&nxt)[NKB]) {
+  // t; each copy has a full iteration to land.  PAR = t % 2 selects buffers;
+  // LEAN selects Softmax::step_lean (hot path) or Softmax::step (exact).
+  auto iteration = [&](auto par, auto lean, auto first, int t, f32x16_t (&cur)[NKB], f32x16_t (&nxt)[NKB]) {
     constexpr int PAR = decltype(par)::value;
+    constexpr bool LEAN = decltype(lean)::value;
+    constexpr bool FIRST = decltype(first)::value;
     constexpr int KNEXT = PAR ? K0 : K1;   // holds K(t+1)
     constexpr int KFREE = PAR ? K1 : K0;   // held K(t), read in the previous iteration
     constexpr int VCUR = PAR ? V1 : V0;    // holds V(t)
@@ -1144,25 +1219,47 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     }
     if (t < nTw) {
       bf16x8_t pb[NK16];
-      sm.step(cur, t, q0, qrow, S, g, cl, o, pb);
+      if constexpr (LEAN)
+        sm.template step_lean<FIRST>(cur, t, q0, qrow, S, g, cl, pb, bad);
+      else
+        sm.step(cur, t, q0, qrow, S, g, cl, o, pb);
       gemm2<D, BN>(smem, VCUR, vra, pb, o);
     }
   };
-
-  f32x16_t sa[NKB], sb[NKB];
-  wait_copies();
-  __syncthreads();
-  if (t0 < nTw) {
-    if constexpr (FK)
-      gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, K0, kra, qreg, sa, p, t0 * BN, g, lr);
-    else
-      gemm1<D, BN>(smem, K0, kra, qreg, sa);
-  }
-  for (int t = t0;;) {
-    iteration(std::integral_constant<int, 0>{}, t, sa, sb);
-    if (++t >= nT) break;
-    iteration(std::integral_constant<int, 1>{}, t, sb, sa);
-    if (++t >= nT) break;
+  // One sweep over the work item's KV tiles; the first K/V copies must have
+  // been issued.
+  auto sweep = [&](auto lean) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
+    sm = Softmax<D, BN, CAUSAL>{};
+    f32x16_t sa[NKB], sb[NKB];
+    wait_copies();
+    __syncthreads();
+    if (t0 < nTw) {
+      if constexpr (FK)
+        gemm1_fused_k<D, BN, ST, PRO == PRO_NORM_ROPE>(smem, K0, kra, qreg, sa, p, t0 * BN, g, lr);
+      else
+        gemm1<D, BN>(smem, K0, kra, qreg, sa);
+    }
+    // the first tile is peeled (it alone reduces the row max on the lean path)
+    iteration(std::integral_constant<int, 0>{}, lean, std::true_type{}, t0, sa, sb);
+    for (int t = t0 + 1; t < nT;) {
+      iteration(std::integral_constant<int, 1>{}, lean, std::false_type{}, t, sb, sa);
+      if (++t >= nT) break;
+      iteration(std::integral_constant<int, 0>{}, lean, std::false_type{}, t, sa, sb);
+      ++t;
+    }
+  };
+  if constexpr (FK) {
+    sweep(std::false_type{});  // mode 'full' runs at the register limit: exact path only
+  } else {
+    sweep(std::true_type{});
+    // A lean tile failed somewhere in the workgroup (a logit far above the
+    // first tile's row max): every wave redoes the item on the exact path.
+    if (__syncthreads_or(bad)) {
+      first_copies();
+      sweep(std::false_type{});
+    }
   }
 
   // the host plans splits for D = 256 only (plan_split)
@@ -1209,7 +1306,16 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   wait_copies();  // every store of this thread has completed
   __syncthreads();
   __shared__ int arrived_before;
-  if (tid == 0) arrived_before = atomicAdd(p.counters + pair, 1);
+  if (tid == 0) {
+    // Release/acquire at agent scope around the arrival counter (the
+    // memory model's own mapping: L2 writeback before, invalidate after), so
+    // the handover is ordered even where the SC1 accesses alone would not
+    // be; one thread per workgroup, after the barrier that follows every
+    // thread's completed stores.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    arrived_before = atomicAdd(p.counters + pair, 1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
   if (arrived_before == 0) return;  // the other half merges
   // Merge in fixed (first half, second half) operand order, whichever half
