@@ -210,8 +210,10 @@ def interleaved(arms: Dict[str, Callable], *, rounds: int = 3, samples: int = 5,
     return res
 
 
-def block_time_us(fn: Callable, launches: int, replays: int = 10, warmups: int = 3) -> float:
+def block_time_us(fn: Callable, launches: int, replays: int = 10, warmups: int = 3, settle_ms: float = 0.0) -> float:
     """Median per-launch device time (us) of ``launches`` calls of ``fn``
-    replayed ``replays`` times as one block (one arm, one round)."""
-    res = interleaved({"arm": fn}, rounds=1, samples=replays, launches=launches, warmups=warmups)
+    replayed ``replays`` times as one block (one arm, one round), after
+    ``settle_ms`` of untimed replays."""
+    res = interleaved({"arm": fn}, rounds=1, samples=replays, launches=launches, warmups=warmups,
+                      settle_ms=settle_ms)
     return res["arms"]["arm"]["median_us"]
