@@ -97,10 +97,11 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
  * For causal D = 256 shapes with no more query blocks than the GPU has CUs
  * (that kernel runs one workgroup per CU), the key range of the longest
  * query blocks is split over two workgroups whose partial results are merged
- * by the one finishing second; the workspace holds those partials and one
- * counter per split block.  The
- * caller zero-fills it once when allocating; each launch leaves the counters
- * at zero again.  Calls that share a workspace must not overlap in time.
+ * by the one finishing second; the workspace holds a 4 KiB region of
+ * arrival counters (the same for every shape) followed by those partials.
+ * The caller zero-fills it once when allocating; each launch leaves the
+ * counters at zero again, so one workspace serves any sequence of shapes
+ * that fit in it.  Calls that share a workspace must not overlap in time.
  * With work == NULL or work_bytes below this size the launch does not split
  * (same results, slower on those shapes).  No counterpart in the reference,
  * whose launches never split a query block. */

@@ -1422,6 +1422,15 @@ int64_t device_cus() {
 // D = 128 two workgroups share each CU and one already keeps it nearly
 // busy, so the extra prologues of a split cost more than the balance gains.
 
+// Workspace layout: a counter region of the same size for every shape (one
+// 4-byte arrival counter per split (block, head) pair, at most
+// SPLIT_MAX_PAIRS; a plan has at most B*Hq*nqb <= CUs pairs), then the
+// partial results.  Because no shape's partials ever land in the counter
+// region and every launch leaves the counters it used at zero, a workspace
+// zero-filled once stays valid for any sequence of shapes launched on it.
+constexpr int64_t SPLIT_MAX_PAIRS = 1024;
+constexpr int64_t SPLIT_COUNTER_BYTES = SPLIT_MAX_PAIRS * 4;
+
 struct SplitPlan {
   int n_items = 0, n_split = 0;
   int16_t qb[MAX_SPLIT_ITEMS], t0[MAX_SPLIT_ITEMS], t1[MAX_SPLIT_ITEMS], sid[MAX_SPLIT_ITEMS];
@@ -1450,7 +1459,7 @@ bool plan_split(int64_t B, int64_t Hq, int64_t S, int64_t D, bool causal, int64_
       items[n++] = {(int)qb, 0, nt, -1};
     }
   }
-  if (n_split == 0) return false;
+  if (n_split == 0 || n_split * B * Hq > SPLIT_MAX_PAIRS) return false;
   // longest first (insertion sort: n <= 128)
   for (int i = 1; i < n; ++i)
     for (int j = i; j > 0 && items[j].t1 - items[j].t0 > items[j - 1].t1 - items[j - 1].t0; --j) {
@@ -1465,7 +1474,6 @@ bool plan_split(int64_t B, int64_t Hq, int64_t S, int64_t D, bool causal, int64_
   return true;
 }
 
-int64_t split_counter_bytes(int64_t pairs) { return (pairs * 4 + 255) / 256 * 256; }
 int64_t split_partial_bytes(int64_t pairs, int64_t D) { return pairs * 2 * (D / 2 + 2) * 256 * 4; }
 
 }  // namespace
@@ -1475,14 +1483,14 @@ int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
   SplitPlan pl;
   if (!plan_split(B, Hq, S, D, causal, device_cus(), pl)) return 0;
   const int64_t pairs = (int64_t)pl.n_split * B * Hq;
-  return split_counter_bytes(pairs) + split_partial_bytes(pairs, D);
+  return SPLIT_COUNTER_BYTES + split_partial_bytes(pairs, D);
 }
 
 int64_t attention_workspace_counter_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal) {
   if (attention_uses_pp(Hq, Hkv, S, D)) return 0;
   SplitPlan pl;
   if (!plan_split(B, Hq, S, D, causal, device_cus(), pl)) return 0;
-  return split_counter_bytes((int64_t)pl.n_split * B * Hq);
+  return SPLIT_COUNTER_BYTES;
 }
 
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
@@ -1527,13 +1535,13 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     SplitPlan pl;
     if (a.work && plan_split(a.B, a.Hq, a.S, a.D, a.causal, device_cus(), pl)) {
       const int64_t pairs = (int64_t)pl.n_split * nbh;
-      if (a.work_bytes >= split_counter_bytes(pairs) + split_partial_bytes(pairs, a.D)) {
+      if (a.work_bytes >= SPLIT_COUNTER_BYTES + split_partial_bytes(pairs, a.D)) {
         p.n_items = pl.n_items;
         for (int i = 0; i < pl.n_items; ++i) {
           p.it_qb[i] = pl.qb[i]; p.it_t0[i] = pl.t0[i]; p.it_t1[i] = pl.t1[i]; p.it_sid[i] = pl.sid[i];
         }
         p.counters = (int *)a.work;
-        p.partials = (float *)((char *)a.work + split_counter_bytes(pairs));
+        p.partials = (float *)((char *)a.work + SPLIT_COUNTER_BYTES);
         blocks = pl.n_items * nbh;
       }
     }

@@ -68,8 +68,9 @@ int64_t attention_workspace_counter_bytes(int64_t B, int64_t Hq, int64_t Hkv, in
 
 // Static split-KV workspace of the allocation-free entry point (one per GPU):
 // 36 MiB covers every causal D = 256 split plan of up to 141 (block, head)
-// pairs, which includes the Gemma-3 geometries up to their largest
-// one-workgroup-per-CU grids (at most 128 pairs, 32.5 MiB).
+// pairs (4 KiB of counters, 260 KiB of partials per pair), which includes
+// the Gemma-3 geometries up to their largest one-workgroup-per-CU grids (at
+// most 128 pairs, 32.5 MiB).
 #define KFMI_SCRATCH_BYTES (36ll << 20)
 // Device address of the current device's static workspace (taken once per
 // device with hipGetSymbolAddress and cached).

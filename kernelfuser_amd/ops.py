@@ -69,7 +69,9 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 # Split-KV workspace (see kfmi_attention_workspace_bytes).  Eager launches use
 # one zero-filled buffer per (device, stream); launches that share it run in
 # that stream's order, so they never overlap on it, and each launch leaves
-# its counters at zero again.  When a larger shape needs more, a new buffer
+# its counters at zero again.  The counter region has the same size for every
+# shape, so the buffer serves any sequence of shapes that fit in it.  When a
+# larger shape needs more, a new buffer
 # replaces it in the cache; the old one stays referenced until the process
 # ends, so nothing that ever held its address sees it freed.  A launch
 # captured into a HIP graph never uses the cache: it gets its own zero-filled

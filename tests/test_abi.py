@@ -114,9 +114,13 @@ def test_workspace_bytes_query(lib):
     assert f(1, 16, 8, 2048, 256, 0) == 0  # not causal: nothing to balance
     assert f(4, 16, 8, 2048, 256, 1) == 0  # more work items than CUs
     n = f(1, 16, 8, 2048, 256, 1)  # 256 items = 256 CUs: the long blocks split
-    # 8 split blocks x 16 heads: counters + 2 halves of 256 threads x (128 + 2) floats
+    # 8 split blocks x 16 heads: a 4 KiB counter region (the same for every
+    # shape) + 2 halves of 256 threads x (128 + 2) floats per pair
     pairs = 8 * 16
-    assert n == (pairs * 4 + 255) // 256 * 256 + pairs * 2 * 130 * 256 * 4
+    assert n == 4096 + pairs * 2 * 130 * 256 * 4
+    # a 12-pair plan keeps the same counter region: its partials start where
+    # the 128-pair plan's do
+    assert f(1, 4, 2, 640, 256, 1) == 4096 + 12 * 2 * 130 * 256 * 4
 
 
 def test_call_maps_einval_to_value_error(lib):

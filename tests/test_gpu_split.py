@@ -109,7 +109,39 @@ def test_split_cached_workspace_per_stream(gpu):
                                   norm_style="fp32")
     torch.cuda.synchronize()
     for out in outs:
-        assert torch.equal(out, ref)
+        bad = out != ref
+        assert not bool(bad.any()), (int(bad.sum()), float((out.float() - ref.float()).abs().max()),
+                                     bad.nonzero()[:4].tolist())
+
+
+def test_workspace_serves_any_shape_sequence(gpu):
+    """One zero-filled workspace serves any sequence of split shapes: the
+    arrival counters sit in a region of the same size for every shape and no
+    shape's partial results land in it.  A 12-pair plan (Hq=4, S=640) run on
+    a workspace sized for a 128-pair plan (Hq=16, S=2048) leaves the larger
+    plan's whole counter region at zero, and the larger shape then gives the
+    same bits as on a fresh workspace."""
+    small = make_inputs(1, 640, (4, 2, 256), 2121).to(gpu)
+    large = make_inputs(1, 2048, (16, 8, 256), 2222).to(gpu)
+    kn_s, kn_l = torch.empty_like(small.k), torch.empty_like(large.k)
+    prepare_attention(small.reference7, None, kn_s, only_k=True, norm_style="fp32")
+    prepare_attention(large.reference7, None, kn_l, only_k=True, norm_style="fp32")
+    nb_s = attention_workspace_bytes(1, 4, 2, 640, 256, True)
+    nb_l = attention_workspace_bytes(1, 16, 8, 2048, 256, True)
+    per_pair = 2 * (256 // 2 + 2) * 256 * 4
+    assert 0 < nb_s < nb_l and nb_l // per_pair == 128 and nb_s // per_pair == 12
+    counter_region = nb_l - (nb_l // per_pair) * per_pair
+    announce("split workspace reused from a 12-pair to a 128-pair plan")
+    work = torch.zeros(nb_l, dtype=torch.uint8, device=gpu)
+    for _ in range(2):
+        _run(small, kn_s, True, work)
+    torch.cuda.synchronize()
+    assert int(work[:counter_region].count_nonzero()) == 0
+    fresh = _run(large, kn_l, True, torch.zeros(nb_l, dtype=torch.uint8, device=gpu))
+    reused = _run(large, kn_l, True, work)
+    torch.cuda.synchronize()
+    assert torch.equal(reused, fresh)
+    assert int(work[:counter_region].count_nonzero()) == 0
 
 
 def test_captured_split_keeps_its_workspace(gpu):
