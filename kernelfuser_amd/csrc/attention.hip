@@ -113,8 +113,12 @@ __device__ __forceinline__ float norm_elem(float x, float inv, float g) {
 template <int ST>
 __device__ __forceinline__ float rope_elem(float n, float np, float c, float s, bool first) {
   if (ST == ST_FP32) {
-    float p0 = __fmul_rn(n, c), p1 = __fmul_rn(np, s);
-    return first ? __fsub_rn(p0, p1) : __fadd_rn(p0, p1);
+    // No contraction into an FMA: both products are rounded, then the sum
+    // (HIP's __fmul_rn/__fadd_rn are plain * and + that the headers let the
+    // compiler contract, so the operators are written here).
+#pragma clang fp contract(off)
+    const float p0 = n * c, p1 = np * s;
+    return first ? p0 - p1 : p0 + p1;
   }
   float p0 = round_bf16(n * c), p1 = round_bf16(np * s);
   return first ? p0 - p1 : p0 + p1;

@@ -4,14 +4,14 @@
 // preparation (src/e1_qk_publication_v3.py:592-609).
 //
 // Memory-bound design:
-//  * a D-wide BF16 row is D/8 lanes x 16 bytes (one 16-lane DPP row for D=128),
-//    so a wave64 covers 64/(D/8) consecutive positions of one head and its
-//    loads/stores are single contiguous runs of 1 KiB;
+//  * a D-wide BF16 row is D/8 lanes x 16 bytes (one 16-lane DPP row for D=128);
+//    rows are taken in memory order, one 16-byte chunk per lane, so a
+//    workgroup covers 256/(D/8) consecutive rows and the grid streams
+//    through each tensor front to back (the same rate at every B and S);
 //  * the sum of squares is reduced with DPP inside the row, the rotate-half
 //    partner (column d +/- D/2) is the lane D/16 away (row_ror:8 for D=128);
-//  * a wave keeps the cos/sin rows of its positions and both gamma vectors in
-//    registers and walks a chunk of heads, so tables are read once per
-//    position per head chunk, not once per row;
+//  * each lane reads its position's cos/sin chunk and the gamma chunks with
+//    cached loads, and the row itself with nontemporal loads and stores;
 //  * FP32 internal arithmetic; the rounding points follow the selected style.
 #include "kfmi_device.h"
 #include "kfmi_launch.h"
@@ -26,9 +26,10 @@ struct RowsParams {
   const uint16_t *v;  // V, transposed into vt by the extra workgroups (VT kernels)
   uint16_t *vt;
   int64_t S;
-  int B, Hq_rows, Hq, Hkv;  // Hq_rows = Q heads processed (0 = K rows only); Hq = Q tensor heads
-  int heads_per_chunk, n_groups;
-  int rows_by;              // grid rows (blockIdx.y) of the row work; VT tiles follow
+  uint32_t s32;             // S
+  uint32_t heads_q, heads_k;  // B*Hq (0 for K-only launches) and B*Hkv
+  uint32_t nblk;              // workgroups per unit of heads (blocks of positions)
+  uint32_t row_blocks;        // workgroups of the row work; V^T tiles follow
   int vt_sblocks;           // 64-row tiles per head of V
   int64_t vt_tiles;         // B * Hkv * vt_sblocks
   float eps;
@@ -97,25 +98,15 @@ __device__ __forceinline__ float norm_elem(float x, float inv, float g) {
 template <int ST>
 __device__ __forceinline__ float rope_elem(float n, float np, float c, float s, bool first) {
   if (ST == ST_FP32) {  // rope:129 / rope:164-167 (fp32=True): two products, one add
-    float p0 = __fmul_rn(n, c), p1 = __fmul_rn(np, s);
-    return first ? __fsub_rn(p0, p1) : __fadd_rn(p0, p1);
+    // No contraction into an FMA: both products are rounded, then the sum
+    // (HIP's __fmul_rn/__fadd_rn are plain * and + that the headers let the
+    // compiler contract, so the operators are written here).
+#pragma clang fp contract(off)
+    const float p0 = n * c, p1 = np * s;
+    return first ? p0 - p1 : p0 + p1;
   }
   float p0 = round_bf16(n * c), p1 = round_bf16(np * s);  // rope:578-579
   return first ? p0 - p1 : p0 + p1;  // rounded to BF16 at the store (rope:580-581)
-}
-
-// Raw 16-byte chunk held by the rotate-half partner lane (lane ^ LPR/2).
-template <int LPR>
-__device__ __forceinline__ u32x4_t partner_chunk(const u32x4_t &x) {
-  u32x4_t r;
-  if constexpr (LPR == 16) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = dpp_u32<DPP_ROW_ROR8>(x[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = (uint32_t)__shfl_xor((int)x[i], LPR / 2);
-  }
-  return r;
 }
 
 template <int LPR>
@@ -125,155 +116,156 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
-// Heads in flight per lane and the wave count the head chunks aim for,
-// tuned on the six-shape sweep (3 and 12288: +2-3% on the B >= 4 shapes
-// over 2 and 16384, the same at B=1).
-#ifndef KFMI_ROWS_U
-#define KFMI_ROWS_U 3
-#endif
-#ifndef KFMI_ROWS_WAVES
-#define KFMI_ROWS_WAVES 12288
-#endif
-// K rows only (the attention path's preparation launch): fewer waves, each
-// covering more heads, so that every wave's table and gamma loads serve at
-// least two rows (4.87 against 5.14 us at B=1, S=4096).
-#ifndef KFMI_ROWS_WAVES_K
-#define KFMI_ROWS_WAVES_K 6144
-#endif
 #ifndef KFMI_ROWS_NT
 #define KFMI_ROWS_NT 1
+#endif
+// Heads per workgroup (rows per lane) of rows_kernel.
+#ifndef KFMI_ROWS_HPW
+#define KFMI_ROWS_HPW 2
 #endif
 __device__ __forceinline__ u32x4_t ld_row(const uint16_t *p) { return KFMI_ROWS_NT ? ld16_nt(p) : ld16(p); }
 __device__ __forceinline__ void st_row(uint16_t *p, const u32x4_t &v) {
   if (KFMI_ROWS_NT) st16_nt(p, v); else st16(p, v);
 }
 
+// Normalised value held by the rotate-half partner lane (lane ^ LPR/2).
+template <int LPR>
+__device__ __forceinline__ float partner_f32(float x) {
+  if constexpr (LPR == 16) return dpp_f32<DPP_ROW_ROR8>(x);
+  else return __shfl_xor(x, LPR / 2);
+}
+
+// A workgroup of 256 threads covers 256/LPR consecutive positions of HPW
+// adjacent heads (Q heads (b, h) of [B,Hq,S,D], absent for K-only launches,
+// then K heads), one 16-byte chunk per lane and head.  Consecutive
+// workgroups take consecutive positions of the same heads, so the rows in
+// flight at any time form one contiguous region of each tensor, whatever B,
+// H and S are.  A lane loads its chunk of each head's row (nontemporal) and
+// its cos/sin and gamma chunks once for all HPW rows (cached loads: the
+// tables and gamma are read once per HPW rows rather than once per row).
+// The rotate-half partner's normalised values come from the partner lane,
+// which computes exactly them for its own chunk.  Lanes past the end (a
+// position >= S, or a head past the tensor's last when HPW does not divide
+// its head count) redo the last position / head and store exactly its bits
+// again, so no load or store is conditional (a conditional store would let
+// the compiler sink the table loads behind the rows' round trip).
 template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
 __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
-  constexpr int LPR = D / 8;     // lanes per row
-  constexpr int RPW = 64 / LPR;  // positions per wave
+  constexpr int LPR = D / 8;      // lanes per row
+  constexpr int RPB = 256 / LPR;  // positions per workgroup
   constexpr int HALF = LPR / 2;
-  constexpr int U = KFMI_ROWS_U;  // heads in flight per lane
+  constexpr int U = KFMI_ROWS_HPW;
+  const uint32_t blk = blockIdx.x;
   if constexpr (VT) {
-    // Grid rows past the row work transpose V tiles (same launch).
-    if ((int)blockIdx.y >= p.rows_by) {
-      const int64_t t = (int64_t)(blockIdx.y - p.rows_by) * gridDim.x + blockIdx.x;
+    // Workgroups past the row work transpose V tiles (same launch).
+    if (blk >= p.row_blocks) {
+      const int64_t t = (int64_t)(blk - p.row_blocks);
       if (t < p.vt_tiles) transpose_tile<D>(p.v, p.vt, p.S, t / p.vt_sblocks, (t % p.vt_sblocks) * 64);
       return;  // workgroup-uniform
     }
   }
-  const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wave >= p.B * p.n_groups) return;  // wave-uniform
-  const int b = wave / p.n_groups;
-  const int64_t pos = (int64_t)(wave % p.n_groups) * RPW + lane / LPR;
-  const int lc = lane % LPR;
-  const int d0 = lc * 8;
-  const int dp = (lc ^ HALF) * 8;  // column of the partner chunk
-  const bool valid = pos < p.S;
+  // Workgroup -> (unit of U heads, block of RPB positions): Q units first.
+  const uint32_t heads_q = ONLY_K ? 0u : p.heads_q;
+  const uint32_t units_q = (heads_q + U - 1) / U;
+  const uint32_t unit = blk / p.nblk;
+  const uint32_t bpos = blk - unit * p.nblk;
+  const bool is_q = unit < units_q;  // workgroup-uniform
+  const uint32_t nh = is_q ? heads_q : p.heads_k;
+  const uint32_t h0 = (is_q ? unit : unit - units_q) * U;
+  uint32_t pos = bpos * RPB + threadIdx.x / LPR;
+  if (pos >= p.s32) pos = p.s32 - 1;
+  const uint32_t lc = threadIdx.x % LPR;
   const bool first = lc < HALF;
-  const int Hq_rows = ONLY_K ? 0 : p.Hq_rows;
-  const int H = Hq_rows + p.Hkv;
-  const int h_begin = blockIdx.y * p.heads_per_chunk;
-  const int h_end = min(H, h_begin + p.heads_per_chunk);
-  const u32x4_t zero = {0u, 0u, 0u, 0u};
+  const char *src = reinterpret_cast<const char *>(is_q ? p.q : p.k);
+  char *dst = reinterpret_cast<char *>(is_q ? p.qn : p.kn);
+  const uint16_t *g = is_q ? p.gq : p.gk;
 
-  float cs[8], sn[8];
-  if (ROPE) {
-    unpack8(valid ? ld16(p.cos + pos * D + d0) : zero, cs);
-    unpack8(valid ? ld16(p.sin + pos * D + d0) : zero, sn);
+  uint32_t off[U];  // byte offsets of the lane's chunks (< 2^32: each tensor has < 2^31 elements)
+  uint32_t row[U];
+  u32x4_t xv[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const uint32_t hh = min(h0 + i, nh - 1);
+    row[i] = hh * p.s32 + pos;
+    off[i] = row[i] * (uint32_t)(2 * D) + lc * 16u;
+    xv[i] = ld_row(reinterpret_cast<const uint16_t *>(src + off[i]));
   }
-  const u32x4_t gq_own = Hq_rows ? ld16(p.gq + d0) : zero;
-  const u32x4_t gq_par = (Hq_rows && ROPE) ? ld16(p.gq + dp) : zero;
-  const u32x4_t gk_own = ld16(p.gk + d0);
-  const u32x4_t gk_par = ROPE ? ld16(p.gk + dp) : zero;
-  const u32x4_t gq_fac = (ST == ST_FACTORED) ? ld16(p.gq + d0) : zero;
+  const u32x4_t g_own = ld16(g + lc * 8);
+  float c[8], sn[8];
+  if constexpr (ROPE) {
+    const uint32_t toff = pos * (uint32_t)(2 * D) + lc * 16u;
+    const u32x4_t cv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.cos) + toff));
+    u32x4_t sv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.sin) + toff));
+    // First half: n*c - np*s; second half: n*c + np*s.  Negating s in the
+    // first half (a sign flip of the BF16 bits, exact) turns both into
+    // n*c + np*s' with the same products and roundings.
+    const uint32_t flip = first ? 0x80008000u : 0u;
+    sv ^= u32x4_t{flip, flip, flip, flip};
+    unpack8(cv, c);
+    unpack8(sv, sn);
+  }
+  float go[8];
+  unpack8(g_own, go);
+  float gq[8];
+  if constexpr (ST == ST_FACTORED) unpack8(ld16(p.gq + lc * 8), gq);
 
-  for (int h0 = h_begin; h0 < h_end; h0 += U) {
-    u32x4_t xv[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int hh = h0 + u;
-      const uint16_t *src = hh < Hq_rows
-                                ? p.q + (((int64_t)b * p.Hq + hh) * p.S + pos) * D + d0
-                                : p.k + (((int64_t)b * p.Hkv + (hh - Hq_rows)) * p.S + pos) * D + d0;
-      xv[u] = (hh < h_end && valid) ? ld_row(src) : zero;
-    }
+  for (int i = 0; i < U; ++i) {
+    float x[8];
+    unpack8(xv[i], x);
+    float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int hh = h0 + u;
-      if (hh >= h_end) break;  // wave-uniform
-      const bool is_q = hh < Hq_rows;
-      float x[8];
-      unpack8(xv[u], x);
-      float ss = 0.f;
+    for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
+    ss = row_sum<LPR>(ss);
+    const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+    if constexpr (ST == ST_FACTORED) {
+      if (is_q) {  // qk:597-601: FP32 inverse RMS per Q row
+        if (lc == 0) p.inv[row[i]] = inv;
+      } else {     // qk:602-609: one rounding of x*inv*gk*gq
+        float y[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
-      ss = row_sum<LPR>(ss);
-      const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
-      const int64_t row = is_q ? ((int64_t)b * p.Hq + hh) * p.S + pos
-                               : ((int64_t)b * p.Hkv + (hh - Hq_rows)) * p.S + pos;
-      if constexpr (ST == ST_FACTORED) {
-        if (is_q) {  // qk:597-601: FP32 inverse RMS per Q row
-          if (valid && lc == 0) p.inv[row] = inv;
-        } else {     // qk:602-609: one rounding of x*inv*gk*gq
-          float gk[8], gq[8], y[8];
-          unpack8(gk_own, gk);
-          unpack8(gq_fac, gq);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), gk[j]), gq[j]);
-          if (valid) st_row(p.kn + row * D + d0, pack8(y));
-        }
-      } else {
-        float go[8], y[8];
-        unpack8(is_q ? gq_own : gk_own, go);
-        if constexpr (ROPE) {
-          float xp[8], gp[8];
-          unpack8(partner_chunk<LPR>(xv[u]), xp);
-          unpack8(is_q ? gq_par : gk_par, gp);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float n = norm_elem<ST>(x[j], inv, go[j]);
-            const float np = norm_elem<ST>(xp[j], inv, gp[j]);
-            y[j] = rope_elem<ST>(n, np, cs[j], sn[j], first);
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) y[j] = norm_elem<ST>(x[j], inv, go[j]);
-        }
-        uint16_t *dst = (is_q ? p.qn : p.kn) + row * D + d0;
-        if (valid) st_row(dst, pack8(y));
+        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), go[j]), gq[j]);
+        st_row(reinterpret_cast<uint16_t *>(dst + off[i]), pack8(y));
       }
+    } else {
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = norm_elem<ST>(x[j], inv, go[j]);
+      if constexpr (ROPE) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = rope_elem<ST>(y[j], partner_f32<LPR>(y[j]), c[j], sn[j], false);
+      }
+      st_row(reinterpret_cast<uint16_t *>(dst + off[i]), pack8(y));
     }
   }
 }
 
 template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
-hipError_t launch_rows_t(const RowsParams &p, int blocks_x, int blocks_y, hipStream_t stream) {
-  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT>), dim3(blocks_x, blocks_y), dim3(256), 0, stream, p);
+hipError_t launch_rows_t(const RowsParams &p, int64_t blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int D, int ST, bool ROPE>
-hipError_t dispatch_k(const RowsParams &p, int bx, int by, hipStream_t s) {
+hipError_t dispatch_k(const RowsParams &p, bool only_k, hipStream_t s) {
   if constexpr (D == 128 && ST != ST_FACTORED) {
     if (p.vt) {
-      const int by_all = by + (int)((p.vt_tiles + bx - 1) / bx);
-      return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false, true>(p, bx, by_all, s)
-                       : launch_rows_t<D, ST, ROPE, true, true>(p, bx, by_all, s);
+      const int64_t all = p.row_blocks + p.vt_tiles;
+      return only_k ? launch_rows_t<D, ST, ROPE, true, true>(p, all, s) : launch_rows_t<D, ST, ROPE, false, true>(p, all, s);
     }
   }
-  return p.Hq_rows ? launch_rows_t<D, ST, ROPE, false, false>(p, bx, by, s)
-                   : launch_rows_t<D, ST, ROPE, true, false>(p, bx, by, s);
+  return only_k ? launch_rows_t<D, ST, ROPE, true, false>(p, p.row_blocks, s)
+                : launch_rows_t<D, ST, ROPE, false, false>(p, p.row_blocks, s);
 }
 
 template <int D>
-hipError_t dispatch_rows(const RowsParams &p, int style, bool rope, int bx, int by, hipStream_t s) {
+hipError_t dispatch_rows(const RowsParams &p, int style, bool rope, bool only_k, hipStream_t s) {
   switch (style) {
-    case ST_HF: return rope ? dispatch_k<D, ST_HF, true>(p, bx, by, s) : dispatch_k<D, ST_HF, false>(p, bx, by, s);
-    case ST_LEGACY: return rope ? dispatch_k<D, ST_LEGACY, true>(p, bx, by, s) : dispatch_k<D, ST_LEGACY, false>(p, bx, by, s);
-    case ST_FP32: return rope ? dispatch_k<D, ST_FP32, true>(p, bx, by, s) : dispatch_k<D, ST_FP32, false>(p, bx, by, s);
-    case ST_FACTORED: return dispatch_k<D, ST_FACTORED, false>(p, bx, by, s);
+    case ST_HF: return rope ? dispatch_k<D, ST_HF, true>(p, only_k, s) : dispatch_k<D, ST_HF, false>(p, only_k, s);
+    case ST_LEGACY:
+      return rope ? dispatch_k<D, ST_LEGACY, true>(p, only_k, s) : dispatch_k<D, ST_LEGACY, false>(p, only_k, s);
+    case ST_FP32: return rope ? dispatch_k<D, ST_FP32, true>(p, only_k, s) : dispatch_k<D, ST_FP32, false>(p, only_k, s);
+    case ST_FACTORED: return dispatch_k<D, ST_FACTORED, false>(p, only_k, s);
   }
   return hipErrorInvalidValue;
 }
@@ -302,30 +294,21 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   p.qn = a.qn; p.kn = a.kn; p.inv = a.inv;
   p.v = a.v; p.vt = a.vt;
   p.S = a.S;
-  p.B = (int)a.B;
-  p.Hq = (int)a.Hq;
-  p.Hq_rows = a.only_k ? 0 : (int)a.Hq;
-  p.Hkv = (int)a.Hkv;
+  p.s32 = (uint32_t)a.S;
   p.eps = a.eps;
-  const int lpr = (int)a.D / 8;
-  const int rpw = 64 / lpr;
-  p.n_groups = (int)((a.S + rpw - 1) / rpw);
-  const int H = p.Hq_rows + p.Hkv;
-  // Split the heads into chunks so the grid holds about the target number of
-  // waves when the position count alone does not.
-  const int64_t waves = (int64_t)p.B * p.n_groups;
-  const int64_t target = a.only_k ? KFMI_ROWS_WAVES_K : KFMI_ROWS_WAVES;
-  int chunks = (int)((target + waves - 1) / waves);
-  chunks = chunks < 1 ? 1 : (chunks > H ? H : chunks);
-  p.heads_per_chunk = (H + chunks - 1) / chunks;
-  const int by = (H + p.heads_per_chunk - 1) / p.heads_per_chunk;
-  const int bx = (int)((waves + 3) / 4);
-  p.rows_by = by;
+  // Each tensor has fewer than 2^31 elements (checked at the boundary), so
+  // row counts and rows*D fit 32 bits.
+  p.heads_q = a.only_k ? 0u : (uint32_t)(a.B * a.Hq);
+  p.heads_k = (uint32_t)(a.B * a.Hkv);
+  const int64_t rpb = 256 / (a.D / 8);
+  p.nblk = (uint32_t)((a.S + rpb - 1) / rpb);
+  const int64_t units = (p.heads_q + KFMI_ROWS_HPW - 1) / KFMI_ROWS_HPW + (p.heads_k + KFMI_ROWS_HPW - 1) / KFMI_ROWS_HPW;
+  p.row_blocks = (uint32_t)(units * p.nblk);
   p.vt_sblocks = (int)((a.S + 63) / 64);
   p.vt_tiles = a.vt ? a.B * a.Hkv * p.vt_sblocks : 0;
   if (a.vt && a.D != 128) return hipErrorInvalidValue;
-  if (a.D == 128) return dispatch_rows<128>(p, a.style, a.rope, bx, by, stream);
-  return dispatch_rows<256>(p, a.style, a.rope, bx, by, stream);
+  if (a.D == 128) return dispatch_rows<128>(p, a.style, a.rope, a.only_k, stream);
+  return dispatch_rows<256>(p, a.style, a.rope, a.only_k, stream);
 }
 
 }  // namespace kfmi
