@@ -32,7 +32,7 @@ from pathlib import Path
 
 import torch
 
-from . import timing
+from . import exclusive, timing
 from .inputs import QWEN3_8B, make_inputs
 
 DEFAULT_ROUNDS, DEFAULT_SAMPLES, DEFAULT_LAUNCHES = 5, 40, 20
@@ -133,9 +133,23 @@ def main(argv=None):
            "rows": []}
     out = Path(args.out)
     out.parent.mkdir(parents=True, exist_ok=True)
+    torch.zeros(1, device="cuda:0")  # hold a context, so the GPU's process list must name this process
+    mon = exclusive.ExclusiveMonitor(0).start()
+    try:
+        _run_rows(batches, sizes, args, rec, mon, out)
+    finally:
+        rec["gpu_exclusivity"] = exclusive.summarize(mon.finish())
+        out.write_text(json.dumps(rec, indent=1) + "\n")
+    return rec
+
+
+def _run_rows(batches, sizes, args, rec, mon, out):
     for b in batches:
         for s in sizes:
+            before = exclusive.gpu_snapshot(0)
+            t0 = time.time()
             row = run_row(b, s, args.rounds, args.samples, args.launches, args.mode, args.norm_style)
+            exclusive.guarded(row, [before, *mon.between(t0, time.time()), exclusive.gpu_snapshot(0)])
             rec["rows"].append(row)
             out.write_text(json.dumps(rec, indent=1) + "\n")
             i, r = row["initial"], row["retest"]
@@ -144,7 +158,6 @@ def main(argv=None):
                   f"{i['paired_ratio_ci95'][1]:.4f}] retest {r['paired_ratio_median']:.4f}", flush=True)
             gc.collect()
             torch.cuda.empty_cache()
-    return rec
 
 
 if __name__ == "__main__":

@@ -282,6 +282,8 @@ def main(argv=None):
     ap.add_argument("--samples", type=int, default=20)
     ap.add_argument("--rounds", type=int, default=5)
     args = ap.parse_args(argv)
+    from . import exclusive
+
     model = load_qwen3(args.model) if args.model else random_qwen3(args.random_layers)
     rec = {"schema": "kernelfuser-amd-qwen3-prefill-v1",
            "model": args.model or f"random Qwen3-8B geometry, {args.random_layers} layers",
@@ -292,7 +294,10 @@ def main(argv=None):
     out.parent.mkdir(parents=True, exist_ok=True)
     for b in args.batches:
         for s in args.sizes:
+            before = exclusive.gpu_snapshot(0)
             row = run_row(model, b, s, samples=args.samples, rounds=args.rounds)
+            row["gpu_before"], row["gpu_after"] = before, exclusive.gpu_snapshot(0)
+            exclusive.guarded(row, [before, row["gpu_after"]])
             rec["rows"].append(row)
             out.write_text(json.dumps(rec, indent=1) + "\n")
             t = row.get("timing", {})

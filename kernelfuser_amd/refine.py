@@ -48,7 +48,7 @@ from pathlib import Path
 
 import torch
 
-from . import timing
+from . import exclusive, timing
 from .inputs import make_inputs
 from .ops import MODELS, launch_attention, launch_factored_attention, prepare_attention
 
@@ -317,9 +317,29 @@ def main(argv=None):
     out = Path(args.out)
     out.parent.mkdir(parents=True, exist_ok=True)
     save = lambda: out.write_text(json.dumps(rec, indent=1) + "\n")
+    torch.zeros(1, device="cuda:0")  # hold a context, so the GPU's process list must name this process
+    rec["gpu_before"] = exclusive.gpu_snapshot(0)
+    mon = exclusive.ExclusiveMonitor(0).start()
+    try:
+        _run_rows(rows, args, rec, mon, save)
+    finally:
+        obs = mon.finish()
+        rec["gpu_after"] = exclusive.gpu_snapshot(0)
+        rec["gpu_exclusivity"] = exclusive.summarize([rec["gpu_before"], *obs, rec["gpu_after"]])
+    bad = [r for r in rec["rows"] if r["status"] != "passed"] + \
+          [t for t in rec.get("tail_checks", []) if not t["pass"]]
+    invalid = [r for r in rec["rows"] if r["status"] == "tested_invalid"]
+    rec["status"] = "passed" if not bad else ("tested_invalid" if len(invalid) == len(bad) else "failed")
+    save()
+    return rec
+
+
+def _run_rows(rows, args, rec, mon, save):
     with torch.inference_mode():
         for model, b, s, causal, rotary in rows:
+            t0 = time.time()
             row = run_row(model, b, s, causal, rotary, launches=args.launches)
+            exclusive.guarded(row, mon.between(t0, time.time()))
             rec["rows"].append(row)
             save()
             sm = row.get("summary")
@@ -334,11 +354,6 @@ def main(argv=None):
             torch.cuda.empty_cache()
         if not args.no_tails:
             rec["tail_checks"] = tail_checks()
-    bad = [r for r in rec["rows"] if r["status"] != "passed"] + \
-          [t for t in rec.get("tail_checks", []) if not t["pass"]]
-    rec["status"] = "passed" if not bad else "failed"
-    save()
-    return rec
 
 
 if __name__ == "__main__":
