@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 5
+#define KFMI_ABI_VERSION 6
 
 /* status codes */
 #define KFMI_OK 0
@@ -59,6 +59,25 @@ int kfmi_abi_version(void);
 
 /* Message of the last failing call on this thread ("" if none). */
 const char *kfmi_last_error(void);
+
+/* One kernel launched by an entry-point call (see kfmi_last_launches). */
+typedef struct {
+  char kernel[96];       /* kernel instance, e.g. "attn_pp_kernel<true, 2, 2, false>" */
+  int64_t grid;          /* workgroups */
+  int32_t block;         /* threads per workgroup */
+  int32_t registers;     /* registers per thread (hipFuncGetAttributes numRegs) */
+  int32_t lds_bytes;     /* static LDS per workgroup */
+  int32_t scratch_bytes; /* private memory per thread (register spills) */
+} kfmi_launch_info;
+
+/* The kernels launched by this thread's last successful compute call, in
+ * launch order: copies up to `max` records into `out` (may be NULL when max
+ * is 0) and returns how many that call launched (0 before any, or after a
+ * call that failed before launching).  Replaces the kernel objects that the
+ * reference's launchers return (launch_attention rope:674-677,
+ * launch_factored_attention qk:651), whose consumer reads registers, spills
+ * and shared memory (fusion_harness.py:82-102 compiler_evidence). */
+int kfmi_last_launches(kfmi_launch_info *out, int max);
 
 /* Row preparation: per-(token,head) RMSNorm(eps) * gamma, then optional
  * rotate-half RoPE, BF16 out.  Replaces prepare_attention -> prepare_kernel

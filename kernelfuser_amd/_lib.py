@@ -14,7 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -70,6 +70,8 @@ def load() -> ctypes.CDLL:
         lib.kfmi_last_error.argtypes = []
         lib.kfmi_attention_workspace_bytes.restype = ctypes.c_int64
         lib.kfmi_attention_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I]
+        lib.kfmi_last_launches.restype = ctypes.c_int
+        lib.kfmi_last_launches.argtypes = [ctypes.POINTER(LaunchInfo), _I]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
@@ -78,6 +80,24 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(f"kfmi ABI version {lib.kfmi_abi_version()} != {ABI_VERSION}")
         _lib = lib
     return _lib
+
+
+class LaunchInfo(ctypes.Structure):
+    """kfmi_launch_info of include/kfmi.h."""
+    _fields_ = [("kernel", ctypes.c_char * 96), ("grid", ctypes.c_int64), ("block", ctypes.c_int32),
+                ("registers", ctypes.c_int32), ("lds_bytes", ctypes.c_int32), ("scratch_bytes", ctypes.c_int32)]
+
+
+def last_launches(max_records: int = 8) -> list[dict]:
+    """The kernels launched by this thread's last successful compute call
+    (kfmi_last_launches), in launch order: kernel instance, workgroups,
+    threads per workgroup, registers per thread, static LDS and scratch bytes."""
+    lib = load()
+    buf = (LaunchInfo * max_records)()
+    n = lib.kfmi_last_launches(buf, max_records)
+    return [{"kernel": r.kernel.decode(errors="replace"), "grid": r.grid, "block": r.block,
+             "registers": r.registers, "lds_bytes": r.lds_bytes, "scratch_bytes": r.scratch_bytes}
+            for r in buf[:min(n, max_records)]]
 
 
 def call(name: str, *args) -> None:

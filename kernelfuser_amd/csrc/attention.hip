@@ -67,6 +67,9 @@
 
 #include <atomic>
 
+#include <cstdio>
+#include <string>
+
 #include "kfmi_device.h"
 #include "kfmi_launch.h"
 
@@ -1348,24 +1351,53 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   if (tid == 0) atomicExch(p.counters + pair, 0);
 }
 
+// Launch-log names of the kernel instances (formatted once per instance).
+template <int D, int BN, bool CAUSAL, int PRO, int ST, bool FK>
+const char *fwd_name() {
+  static const std::string n = [] {
+    char b[96];
+    snprintf(b, sizeof(b), "attn_fwd_kernel<%d, %d, %s, %d, %d, %s>", D, BN, tf(CAUSAL), PRO, ST, tf(FK));
+    return std::string(b);
+  }();
+  return n.c_str();
+}
+template <bool CAUSAL, int PRO, int ST, bool VT>
+const char *pp_name() {
+  static const std::string n = [] {
+    char b[96];
+    snprintf(b, sizeof(b), "attn_pp_kernel<%s, %d, %d, %s>", tf(CAUSAL), PRO, ST, tf(VT));
+    return std::string(b);
+  }();
+  return n.c_str();
+}
+
 template <int D, int BN, bool CAUSAL, int PRO, int ST>
 hipError_t launch_t(const AttnParams &p, bool pp, int blocks, hipStream_t s) {
   if constexpr (PRO == PRO_NORM || PRO == PRO_NORM_ROPE) {
     if (p.gk) {  // mode 'full': general kernel with the per-tile K prologue
       hipLaunchKernelGGL((attn_fwd_kernel<D, BN, CAUSAL, PRO, ST, true>), dim3(blocks), dim3(256), 0, s, p);
+      launch_log_add(reinterpret_cast<const void *>(&attn_fwd_kernel<D, BN, CAUSAL, PRO, ST, true>),
+                     fwd_name<D, BN, CAUSAL, PRO, ST, true>(), blocks, 256);
       return hipGetLastError();
     }
   }
   if constexpr (D == 128) {
     if (pp) {
-      if (p.vt)
+      if (p.vt) {
         hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST, true>), dim3(blocks), dim3(512), 0, s, p);
-      else
+        launch_log_add(reinterpret_cast<const void *>(&attn_pp_kernel<CAUSAL, PRO, ST, true>),
+                       pp_name<CAUSAL, PRO, ST, true>(), blocks, 512);
+      } else {
         hipLaunchKernelGGL((attn_pp_kernel<CAUSAL, PRO, ST, false>), dim3(blocks), dim3(512), 0, s, p);
+        launch_log_add(reinterpret_cast<const void *>(&attn_pp_kernel<CAUSAL, PRO, ST, false>),
+                       pp_name<CAUSAL, PRO, ST, false>(), blocks, 512);
+      }
       return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((attn_fwd_kernel<D, BN, CAUSAL, PRO, ST>), dim3(blocks), dim3(256), 0, s, p);
+  launch_log_add(reinterpret_cast<const void *>(&attn_fwd_kernel<D, BN, CAUSAL, PRO, ST, false>),
+                 fwd_name<D, BN, CAUSAL, PRO, ST, false>(), blocks, 256);
   return hipGetLastError();
 }
 

@@ -12,9 +12,13 @@
 #include "kfmi.h"
 #include "kfmi_launch.h"
 
+#include <unordered_map>
+#include <vector>
+
 namespace {
 
 thread_local std::string g_error;
+thread_local std::vector<kfmi_launch_info> g_launches;
 
 int fail(int code, const char *fmt, ...) {
   char buf[512];
@@ -23,6 +27,7 @@ int fail(int code, const char *fmt, ...) {
   vsnprintf(buf, sizeof(buf), fmt, ap);
   va_end(ap);
   g_error = buf;
+  g_launches.clear();  // a failed call reports no launches
   return code;
 }
 
@@ -32,8 +37,48 @@ int launch_status(hipError_t e, const char *what) {
   return KFMI_OK;
 }
 
-// gfx950 check of the current device, cached per device ordinal.
+}  // namespace
+
+namespace kfmi {
+
+void launch_log_clear() { g_launches.clear(); }
+
+void launch_log_add(const void *fn, const char *name, int64_t grid, int block) {
+  // hipFuncGetAttributes once per kernel instance (the figures do not change)
+  static std::mutex mu;
+  static std::unordered_map<const void *, hipFuncAttributes> cache;
+  hipFuncAttributes attr{};
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(fn);
+    if (it == cache.end()) {
+      if (hipFuncGetAttributes(&attr, fn) != hipSuccess) {
+        (void)hipGetLastError();  // a failed query must not look like a failed launch
+        attr = hipFuncAttributes{};
+      }
+      it = cache.emplace(fn, attr).first;
+    }
+    attr = it->second;
+  }
+  kfmi_launch_info r{};
+  snprintf(r.kernel, sizeof(r.kernel), "%s", name);
+  r.grid = grid;
+  r.block = block;
+  r.registers = attr.numRegs;
+  r.lds_bytes = (int32_t)attr.sharedSizeBytes;
+  r.scratch_bytes = (int32_t)attr.localSizeBytes;
+  g_launches.push_back(r);
+}
+
+}  // namespace kfmi
+
+namespace {
+
+// gfx950 check of the current device, cached per device ordinal.  Every
+// compute entry point calls it after its argument checks, right before it
+// launches, so this is also where the call's launch log starts.
 int check_device() {
+  kfmi::launch_log_clear();
   static std::mutex mu;
   static int cached[64];  // 0 unknown, 1 ok, 2 wrong arch
   int dev = 0;
@@ -100,6 +145,12 @@ extern "C" {
 int kfmi_abi_version(void) { return KFMI_ABI_VERSION; }
 
 const char *kfmi_last_error(void) { return g_error.c_str(); }
+
+int kfmi_last_launches(kfmi_launch_info *out, int max) {
+  const int n = (int)g_launches.size();
+  for (int i = 0; i < n && i < max && out; ++i) out[i] = g_launches[i];
+  return n;
+}
 
 int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk, const void *cos,
                       const void *sin, void *qn, void *kn, void *vt, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,

@@ -52,6 +52,13 @@ struct AttnArgs {
 };
 
 // Both return hipSuccess or the launch error.  Arguments are validated by the caller.
+// Launch log of the calling thread: each C-ABI compute entry point clears it
+// once its arguments are valid, and every kernel launch appends the kernel
+// instance, its grid and block and the runtime's resource figures for it.
+void launch_log_clear();
+void launch_log_add(const void *fn, const char *name, int64_t grid, int block);
+inline const char *tf(bool b) { return b ? "true" : "false"; }
+
 hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
 // vt[b,h,d,s] = v[b,h,s,d] for the B*H heads of S rows of D.
 hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64_t S, int64_t D, hipStream_t stream);

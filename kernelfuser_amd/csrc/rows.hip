@@ -13,6 +13,9 @@
 //  * each lane reads its position's cos/sin chunk and the gamma chunks with
 //    cached loads, and the row itself with nontemporal loads and stores;
 //  * FP32 internal arithmetic; the rounding points follow the selected style.
+#include <cstdio>
+#include <string>
+
 #include "kfmi_device.h"
 #include "kfmi_launch.h"
 
@@ -243,6 +246,12 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
 template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
 hipError_t launch_rows_t(const RowsParams &p, int64_t blocks, hipStream_t stream) {
   hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  static const std::string name = [] {
+    char b[96];
+    snprintf(b, sizeof(b), "rows_kernel<%d, %d, %s, %s, %s>", D, ST, tf(ROPE), tf(ONLY_K), tf(VT));
+    return std::string(b);
+  }();
+  launch_log_add(reinterpret_cast<const void *>(&rows_kernel<D, ST, ROPE, ONLY_K, VT>), name.c_str(), blocks, 256);
   return hipGetLastError();
 }
 
@@ -282,8 +291,12 @@ hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64
   const dim3 grid((unsigned)((S + 63) / 64), (unsigned)BH);
   if (D == 128) {
     hipLaunchKernelGGL((transpose_v_kernel<128>), grid, dim3(256), 0, stream, v, vt, S);
+    launch_log_add(reinterpret_cast<const void *>(&transpose_v_kernel<128>), "transpose_v_kernel<128>",
+                   (int64_t)grid.x * grid.y, 256);
   } else {
     hipLaunchKernelGGL((transpose_v_kernel<256>), grid, dim3(256), 0, stream, v, vt, S);
+    launch_log_add(reinterpret_cast<const void *>(&transpose_v_kernel<256>), "transpose_v_kernel<256>",
+                   (int64_t)grid.x * grid.y, 256);
   }
   return hipGetLastError();
 }

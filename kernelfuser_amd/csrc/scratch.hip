@@ -59,6 +59,7 @@ hipError_t clear_scratch_words(void *addr, int64_t bytes, hipStream_t stream) {
   const int n = (int)(bytes / 4);
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, stream, (uint32_t *)addr, n);
+  launch_log_add(reinterpret_cast<const void *>(&zero_words_kernel), "zero_words_kernel", 1, 256);
   return hipGetLastError();
 }
 

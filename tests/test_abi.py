@@ -26,7 +26,7 @@ def lib():
 
 def test_header_declares_the_bound_entry_points():
     names = _declared()
-    queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes"}
+    queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes", "kfmi_last_launches"}
     assert queries <= set(names)
     assert set(_lib.SIGNATURES) == set(names) - queries
 
@@ -141,3 +141,9 @@ def test_last_error_is_per_thread(lib):
     t.start()
     t.join()
     assert seen["msg"] == "" and "multiple of 8" in _err(lib)
+
+
+def test_failed_call_reports_no_launches(lib):
+    lib.kfmi_transpose_v_bf16(P, P, 4, 100, 128, None)  # rejected before any launch
+    assert lib.kfmi_last_launches(None, 0) == 0
+    assert _lib.last_launches() == []

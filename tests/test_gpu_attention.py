@@ -310,3 +310,26 @@ def test_mode_full(gpu, geom, b, s, causal, style, rope):
     d = (out_f.float() - out_q.float()).abs()
     assert float(d.max()) <= 2e-2, float(d.max())
     assert float(d.mean()) <= 1e-3, float(d.mean())
+
+
+def test_launchers_return_their_kernels(gpu):
+    """launch_attention / launch_factored_attention / prepare_attention return
+    the launched kernels (instance, grid, block, registers, LDS, scratch) where
+    the reference returns its kernel object (rope:674-677, qk:651)."""
+    from kernelfuser_amd import launch_factored_attention, prepare_attention
+    xs = make_inputs(1, 4096, QWEN3_8B, 31).to(gpu)
+    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    announce("launch records B=1 S=4096 query")
+    recs = launch_attention(xs.reference7, out, causal=True, mode="query", kn=kn, norm_style="fp32")
+    assert [r["kernel"] for r in recs] == ["rows_kernel<128, 2, true, true, false>",
+                                           "attn_pp_kernel<true, 2, 2, false>"]
+    assert recs[0]["block"] == 256 and recs[1]["block"] == 512 and recs[1]["grid"] == 256
+    assert recs[1]["lds_bytes"] == 131072 and all(r["registers"] > 0 and r["scratch_bytes"] == 0 for r in recs)
+    prep = prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+    assert [r["kernel"] for r in prep] == [recs[0]["kernel"]]
+    fx = make_inputs(1, 256, (8, 4, 256), 32, rope=False).to(gpu)
+    inv = torch.empty(fx.q.shape[:-1], device=gpu, dtype=torch.float32)
+    f = launch_factored_attention((fx.q, fx.k, fx.v, fx.gq, fx.gk), torch.empty_like(fx.q), inv,
+                                  torch.empty_like(fx.k), causal=True)
+    torch.cuda.synchronize()
+    assert [r["kernel"].split("<")[0] for r in f] == ["rows_kernel", "attn_fwd_kernel"]
