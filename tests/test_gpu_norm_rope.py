@@ -142,3 +142,37 @@ def test_full_size_row_sample(gpu, b, s):
     pre = nq[..., : d // 2].square() + nq[..., d // 2:].square()
     post = qn.float()[..., : d // 2].square() + qn.float()[..., d // 2:].square()
     assert bool(((post - pre).abs() <= pre * 2.0 ** -6 + 1e-3).all())
+
+
+@pytest.mark.parametrize("style", ["fp32", "hf"])
+@pytest.mark.parametrize("b,s,geom", [(1, 1, (3, 1, 128)), (1, 15, (3, 1, 128)), (3, 33, (1, 1, 128)),
+                                      (1, 9, (3, 1, 256)), (2, 17, (5, 5, 128))])
+def test_odd_heads_and_ragged_positions(gpu, style, b, s, geom):
+    """The row kernel takes two heads and 256/(D/8) positions per workgroup.
+    Odd head counts (the second head past a tensor's last) and S not a
+    multiple of the block (positions past S) redo the last head / row and
+    store exactly its bits: outputs match the oracle, and nothing outside the
+    output tensors is written (they are views inside sentinel-filled buffers)."""
+    xs = make_inputs(b, s, geom, 5151)
+    q, k, gq, gk, cos, sin = (t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin))
+    pad = 4096  # elements (8 KiB) on each side
+    bufs = [torch.full((t.numel() + 2 * pad,), 7.0, dtype=torch.bfloat16, device=gpu) for t in (q, k)]
+    qn, kn = (buf[pad:pad + t.numel()].view(t.shape) for buf, t in zip(bufs, (q, k)))
+    announce(f"norm_rope {style} odd heads B={b} S={s} geom={geom}")
+    norm_rope(q, k, gq, gk, cos, sin, norm_style=style, qn=qn, kn=kn)
+    torch.cuda.synchronize()
+    for buf in bufs:
+        assert bool((buf[:pad] == 7.0).all()) and bool((buf[-pad:] == 7.0).all())
+    if style == "fp32":
+        for got, ref in zip((qn, kn), _oracle_fp32(xs)):
+            m = oracle.norm_rope_gate(got.cpu(), ref)
+            assert m["pass"], m
+    else:
+        for got, (ref, scale) in zip((qn.cpu(), kn.cpu()), _oracle_chain(xs, style)):
+            diff = (got.float() - ref.float()).abs()
+            assert bool((diff <= bf16_ulp(scale) + bf16_ulp(ref)).all())
+    # K-only preparation of the same odd head count
+    kn2 = torch.empty_like(k)
+    prepare_attention((q, k, None, gq, gk, cos, sin), None, kn2, only_k=True, rope=True, norm_style=style)
+    torch.cuda.synchronize()
+    assert torch.equal(kn2, kn)
