@@ -28,7 +28,12 @@ def test_qwen3_prefill_gates(model, b, s):
     m = row["correctness"]
     assert m["pass_noise_floor"] and m["nll_abs_diff"] <= 2.5e-2 and m["relative_l2"] <= 2.5e-2
     if b == 1:
-        assert row["timing"]["candidate_median_us"] > 0 and row["timing"]["speedup_paired_median"] > 0
+        # timed against the vendor baseline (the unpatched HF attention, BF16
+        # SDPA on its fused kernels), which is itself gated on the noise floor
+        assert "vendor" in row
+        if "error" not in row["vendor"]:
+            assert row["vendor"]["pass_noise_floor"], row["vendor"]
+            assert row["timing"]["candidate_median_us"] > 0 and row["timing"]["speedup_paired_median"] > 0
 
 
 def test_patch_restore(model):
