@@ -149,9 +149,8 @@ __device__ __forceinline__ float partner_f32(float x) {
 // The rotate-half partner's normalised values come from the partner lane,
 // which computes exactly them for its own chunk.  Lanes past the end (a
 // position >= S, or a head past the tensor's last when HPW does not divide
-// its head count) redo the last position / head and store exactly its bits
-// again, so no load or store is conditional (a conditional store would let
-// the compiler sink the table loads behind the rows' round trip).
+// its head count) load the last position / head, so every load stays in
+// bounds and unconditional, and store nothing (outputs may alias inputs).
 template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
 __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   constexpr int LPR = D / 8;      // lanes per row
@@ -176,7 +175,8 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   const uint32_t nh = is_q ? heads_q : p.heads_k;
   const uint32_t h0 = (is_q ? unit : unit - units_q) * U;
   uint32_t pos = bpos * RPB + threadIdx.x / LPR;
-  if (pos >= p.s32) pos = p.s32 - 1;
+  const bool pvalid = pos < p.s32;
+  if (!pvalid) pos = p.s32 - 1;  // loads stay in bounds; nothing is stored for this lane
   const uint32_t lc = threadIdx.x % LPR;
   const bool first = lc < HALF;
   const char *src = reinterpret_cast<const char *>(is_q ? p.q : p.k);
@@ -194,11 +194,19 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
     xv[i] = ld_row(reinterpret_cast<const uint16_t *>(src + off[i]));
   }
   const u32x4_t g_own = ld16(g + lc * 8);
-  float c[8], sn[8];
+  u32x4_t cv, sv, gqv;
   if constexpr (ROPE) {
     const uint32_t toff = pos * (uint32_t)(2 * D) + lc * 16u;
-    const u32x4_t cv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.cos) + toff));
-    u32x4_t sv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.sin) + toff));
+    cv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.cos) + toff));
+    sv = ld16(reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(p.sin) + toff));
+  }
+  if constexpr (ST == ST_FACTORED) gqv = ld16(p.gq + lc * 8);
+  // Every load is issued before the rows' round trip: the stores below are
+  // conditional, and without this barrier the compiler sinks the table loads
+  // into their branch, behind the wait for the rows.
+  asm volatile("" ::: "memory");
+  float c[8], sn[8];
+  if constexpr (ROPE) {
     // First half: n*c - np*s; second half: n*c + np*s.  Negating s in the
     // first half (a sign flip of the BF16 bits, exact) turns both into
     // n*c + np*s' with the same products and roundings.
@@ -210,8 +218,13 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   float go[8];
   unpack8(g_own, go);
   float gq[8];
-  if constexpr (ST == ST_FACTORED) unpack8(ld16(p.gq + lc * 8), gq);
+  if constexpr (ST == ST_FACTORED) unpack8(gqv, gq);
 
+  // Both rows are computed before either is stored: loads and stores share
+  // vmcnt, so a store issued between the rows would make the second row's
+  // wait for its load also wait for the first row's store.
+  u32x4_t yv[U];
+  float invr[U];
 #pragma unroll
   for (int i = 0; i < U; ++i) {
     float x[8];
@@ -221,24 +234,35 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
     for (int j = 0; j < 8; ++j) ss = __fmaf_rn(x[j], x[j], ss);
     ss = row_sum<LPR>(ss);
     const float inv = rsqrt_rn(ss * (1.0f / D) + p.eps);
+    invr[i] = inv;
+    float y[8];
     if constexpr (ST == ST_FACTORED) {
-      if (is_q) {  // qk:597-601: FP32 inverse RMS per Q row
-        if (lc == 0) p.inv[row[i]] = inv;
-      } else {     // qk:602-609: one rounding of x*inv*gk*gq
-        float y[8];
+      // qk:602-609 (K rows): one rounding of x*inv*gk*gq; Q rows keep only inv
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), go[j]), gq[j]);
-        st_row(reinterpret_cast<uint16_t *>(dst + off[i]), pack8(y));
-      }
+      for (int j = 0; j < 8; ++j) y[j] = __fmul_rn(__fmul_rn(__fmul_rn(x[j], inv), go[j]), gq[j]);
     } else {
-      float y[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = norm_elem<ST>(x[j], inv, go[j]);
       if constexpr (ROPE) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) y[j] = rope_elem<ST>(y[j], partner_f32<LPR>(y[j]), c[j], sn[j], false);
       }
-      st_row(reinterpret_cast<uint16_t *>(dst + off[i]), pack8(y));
+    }
+    yv[i] = pack8(y);
+    // The rows are finished here, with every lane active: otherwise the
+    // compiler sinks their arithmetic into the store branches below, where
+    // the partner exchange (DPP, which needs every lane) no longer folds
+    // into the multiplies.
+    asm volatile("" ::"v"(yv[i]), "v"(invr[i]));
+  }
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    // a lane past S, or a second head past the tensor's last, stores nothing
+    if (!(pvalid && h0 + i < nh)) continue;
+    if (ST == ST_FACTORED && is_q) {  // qk:597-601: FP32 inverse RMS per Q row
+      if (lc == 0) p.inv[row[i]] = invr[i];
+    } else {
+      st_row(reinterpret_cast<uint16_t *>(dst + off[i]), yv[i]);
     }
   }
 }

@@ -176,3 +176,20 @@ def test_odd_heads_and_ragged_positions(gpu, style, b, s, geom):
     prepare_attention((q, k, None, gq, gk, cos, sin), None, kn2, only_k=True, rope=True, norm_style=style)
     torch.cuda.synchronize()
     assert torch.equal(kn2, kn)
+
+
+@pytest.mark.parametrize("b,s,geom", [(1, 33, (3, 1, 128)), (2, 17, (5, 5, 128)), (1, 9, (3, 1, 256)), (2, 200, QWEN3_8B)])
+def test_in_place_outputs(gpu, b, s, geom):
+    """Outputs may alias the inputs (qn=q, kn=k): a lane reads only its own
+    rows before writing them, and lanes past S or past the last head write
+    nothing, so the in-place result equals the out-of-place one bit for bit."""
+    xs = make_inputs(b, s, geom, 6161)
+    q, k, gq, gk, cos, sin = (t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin))
+    announce(f"norm_rope in place B={b} S={s} geom={geom}")
+    ref_q, ref_k = norm_rope(q, k, gq, gk, cos, sin, norm_style="fp32")
+    qi, ki = q.clone(), k.clone()
+    norm_rope(qi, ki, gq, gk, cos, sin, norm_style="fp32", qn=qi, kn=ki)
+    kk = k.clone()
+    prepare_attention((q, kk, None, gq, gk, cos, sin), None, kk, only_k=True, rope=True, norm_style="fp32")
+    torch.cuda.synchronize()
+    assert torch.equal(qi, ref_q) and torch.equal(ki, ref_k) and torch.equal(kk, ref_k)
