@@ -32,6 +32,7 @@ struct RowsParams {
   uint32_t s32;             // S
   uint32_t heads_q, heads_k;  // B*Hq (0 for K-only launches) and B*Hkv
   uint32_t nblk;              // workgroups per unit of heads (blocks of positions)
+  int hpw;                    // heads per workgroup (the kernel instance's U)
   uint32_t row_blocks;        // workgroups of the row work; V^T tiles follow
   int vt_sblocks;           // 64-row tiles per head of V
   int64_t vt_tiles;         // B * Hkv * vt_sblocks
@@ -122,10 +123,13 @@ __device__ __forceinline__ float row_sum(float x) {
 #ifndef KFMI_ROWS_NT
 #define KFMI_ROWS_NT 1
 #endif
-// Heads per workgroup (rows per lane) of rows_kernel.
-#ifndef KFMI_ROWS_HPW
-#define KFMI_ROWS_HPW 2
-#endif
+// Heads per workgroup (rows per lane) of rows_kernel: two, or four for
+// Q+K launches of at least 2^18 rows with S <= 4096 at D = 128 (1.2-1.5
+// points of HBM peak more at B >= 4, S <= 2048; 0.8 less at B = 1, S = 8192;
+// fewer, longer workgroups lose on small launches, and the K-only
+// preparation is faster with two).
+constexpr int ROWS_HPW = 2, ROWS_HPW_BIG = 4;
+constexpr int64_t ROWS_BIG = (int64_t)1 << 18, ROWS_BIG_MAX_S = 4096;
 __device__ __forceinline__ u32x4_t ld_row(const uint16_t *p) { return KFMI_ROWS_NT ? ld16_nt(p) : ld16(p); }
 __device__ __forceinline__ void st_row(uint16_t *p, const u32x4_t &v) {
   if (KFMI_ROWS_NT) st16_nt(p, v); else st16(p, v);
@@ -151,12 +155,11 @@ __device__ __forceinline__ float partner_f32(float x) {
 // position >= S, or a head past the tensor's last when HPW does not divide
 // its head count) load the last position / head, so every load stays in
 // bounds and unconditional, and store nothing (outputs may alias inputs).
-template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
+template <int D, int ST, bool ROPE, bool ONLY_K, bool VT, int U>
 __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   constexpr int LPR = D / 8;      // lanes per row
   constexpr int RPB = 256 / LPR;  // positions per workgroup
   constexpr int HALF = LPR / 2;
-  constexpr int U = KFMI_ROWS_HPW;
   const uint32_t blk = blockIdx.x;
   if constexpr (VT) {
     // Workgroups past the row work transpose V tiles (same launch).
@@ -267,15 +270,15 @@ __global__ __launch_bounds__(256) void rows_kernel(RowsParams p) {
   }
 }
 
-template <int D, int ST, bool ROPE, bool ONLY_K, bool VT>
+template <int D, int ST, bool ROPE, bool ONLY_K, bool VT, int U = ROWS_HPW>
 hipError_t launch_rows_t(const RowsParams &p, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((rows_kernel<D, ST, ROPE, ONLY_K, VT, U>), dim3((unsigned)blocks), dim3(256), 0, stream, p);
   static const std::string name = [] {
     char b[96];
-    snprintf(b, sizeof(b), "rows_kernel<%d, %d, %s, %s, %s>", D, ST, tf(ROPE), tf(ONLY_K), tf(VT));
+    snprintf(b, sizeof(b), "rows_kernel<%d, %d, %s, %s, %s, %d>", D, ST, tf(ROPE), tf(ONLY_K), tf(VT), U);
     return std::string(b);
   }();
-  launch_log_add(reinterpret_cast<const void *>(&rows_kernel<D, ST, ROPE, ONLY_K, VT>), name.c_str(), blocks, 256);
+  launch_log_add(reinterpret_cast<const void *>(&rows_kernel<D, ST, ROPE, ONLY_K, VT, U>), name.c_str(), blocks, 256);
   return hipGetLastError();
 }
 
@@ -286,6 +289,7 @@ hipError_t dispatch_k(const RowsParams &p, bool only_k, hipStream_t s) {
       const int64_t all = p.row_blocks + p.vt_tiles;
       return only_k ? launch_rows_t<D, ST, ROPE, true, true>(p, all, s) : launch_rows_t<D, ST, ROPE, false, true>(p, all, s);
     }
+    if (p.hpw == ROWS_HPW_BIG) return launch_rows_t<D, ST, ROPE, false, false, ROWS_HPW_BIG>(p, p.row_blocks, s);
   }
   return only_k ? launch_rows_t<D, ST, ROPE, true, false>(p, p.row_blocks, s)
                 : launch_rows_t<D, ST, ROPE, false, false>(p, p.row_blocks, s);
@@ -339,7 +343,10 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   p.heads_k = (uint32_t)(a.B * a.Hkv);
   const int64_t rpb = 256 / (a.D / 8);
   p.nblk = (uint32_t)((a.S + rpb - 1) / rpb);
-  const int64_t units = (p.heads_q + KFMI_ROWS_HPW - 1) / KFMI_ROWS_HPW + (p.heads_k + KFMI_ROWS_HPW - 1) / KFMI_ROWS_HPW;
+  const int64_t rows = (int64_t)(p.heads_q + p.heads_k) * a.S;
+  p.hpw = (a.D == 128 && !a.only_k && !a.vt && a.style != ST_FACTORED && rows >= ROWS_BIG &&
+            a.S <= ROWS_BIG_MAX_S) ? ROWS_HPW_BIG : ROWS_HPW;
+  const int64_t units = (p.heads_q + p.hpw - 1) / p.hpw + (p.heads_k + p.hpw - 1) / p.hpw;
   p.row_blocks = (uint32_t)(units * p.nblk);
   p.vt_sblocks = (int)((a.S + 63) / 64);
   p.vt_tiles = a.vt ? a.B * a.Hkv * p.vt_sblocks : 0;

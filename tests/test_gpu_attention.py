@@ -321,7 +321,7 @@ def test_launchers_return_their_kernels(gpu):
     out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
     announce("launch records B=1 S=4096 query")
     recs = launch_attention(xs.reference7, out, causal=True, mode="query", kn=kn, norm_style="fp32")
-    assert [r["kernel"] for r in recs] == ["rows_kernel<128, 2, true, true, false>",
+    assert [r["kernel"] for r in recs] == ["rows_kernel<128, 2, true, true, false, 2>",
                                            "attn_pp_kernel<true, 2, 2, false>"]
     assert recs[0]["block"] == 256 and recs[1]["block"] == 512 and recs[1]["grid"] == 256
     assert recs[1]["lds_bytes"] == 131072 and all(r["registers"] > 0 and r["scratch_bytes"] == 0 for r in recs)

@@ -193,3 +193,24 @@ def test_in_place_outputs(gpu, b, s, geom):
     prepare_attention((q, kk, None, gq, gk, cos, sin), None, kk, only_k=True, rope=True, norm_style="fp32")
     torch.cuda.synchronize()
     assert torch.equal(qi, ref_q) and torch.equal(ki, ref_k) and torch.equal(kk, ref_k)
+
+
+def test_large_launch_four_heads_odd_and_in_place(gpu):
+    """Q+K launches of at least 2^18 rows with S <= 4096 take four heads per
+    workgroup: with B=10 and 7 Q and 7 K heads (70 heads per tensor, a partial
+    last unit) and S = 1873 (a partial last block), the result passes the
+    oracle gate, equals the in-place result bit for bit, and the launch
+    record names the instance."""
+    from kernelfuser_amd import _lib
+    xs = make_inputs(10, 1873, (7, 7, 128), 7171)
+    q, k, gq, gk, cos, sin = (t.to(gpu) for t in (xs.q, xs.k, xs.gq, xs.gk, xs.cos, xs.sin))
+    announce("norm_rope four heads per workgroup, B=10, 7+7 heads, S=1873")
+    qn, kn = norm_rope(q, k, gq, gk, cos, sin, norm_style="fp32")
+    assert _lib.last_launches()[0]["kernel"] == "rows_kernel<128, 2, true, false, false, 4>"
+    qi, ki = q.clone(), k.clone()
+    norm_rope(qi, ki, gq, gk, cos, sin, norm_style="fp32", qn=qi, kn=ki)
+    torch.cuda.synchronize()
+    assert torch.equal(qi, qn) and torch.equal(ki, kn)
+    for got, ref in zip((qn, kn), _oracle_fp32(xs)):
+        m = oracle.norm_rope_gate(got.cpu(), ref)
+        assert m["pass"], m
