@@ -274,17 +274,20 @@ def pmc_run(torch, kf):
     for _ in range(3):
         kf.launch_factored_attention((fx.q, fx.k, fx.v, fx.gq, fx.gk), fo, finv, fk, causal=True, bm=128, bn=64)
     del fx, fo, fk, finv
-    nr = kf.make_inputs(1, 8192, QWEN3_8B, 1909, with_v=False).to("cuda:0")
-    qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
-    for _ in range(3):
-        kf.norm_rope(nr.q, nr.k, nr.gq, nr.gk, nr.cos, nr.sin, norm_style="fp32", qn=qn, kn=kn2)
+    # norm+RoPE: B=1 S=8192 runs two heads per workgroup, B=4 S=2048 four
+    for b, s in ((1, 8192), (4, 2048)):
+        nr = kf.make_inputs(b, s, QWEN3_8B, 1909, with_v=False).to("cuda:0")
+        qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
+        for _ in range(3):
+            kf.norm_rope(nr.q, nr.k, nr.gq, nr.gk, nr.cos, nr.sin, norm_style="fp32", qn=qn, kn=kn2)
+        del nr, qn, kn2
     src = torch.ones(256 * 2 ** 20 // 4, device="cuda:0", dtype=torch.float32)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_run": True, "copy_bytes_each_way": src.numel() * 4,
-                      "attention": "B=1 S=4096 causal", "general": ["B=1 S=2048", "B=4 S=1000", "factored D=256 B=2 S=2048"], "norm_rope": "B=1 S=8192"}), flush=True)
+                      "attention": "B=1 S=4096 causal", "general": ["B=1 S=2048", "B=4 S=1000", "factored D=256 B=2 S=2048"], "norm_rope": ["B=1 S=8192", "B=4 S=2048"]}), flush=True)
 
 
 def main():
