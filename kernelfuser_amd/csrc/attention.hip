@@ -5,14 +5,15 @@
 //
 // Two kernels share the arithmetic below:
 //   attn_pp_kernel   D=128, Hq/Hkv even (the Qwen3 shapes).  One workgroup =
-//                    8 waves = two Q heads of one GQA group x 128 query rows.
+//                    8 waves = two Q heads of one GQA group x 128 query rows,
+//                    or, when Hq/Hkv is a multiple of 4, four heads x 64 rows.
 //                    Waves w and w+4 run on the same SIMD; group A (waves 0-3,
-//                    first head) and group B (waves 4-7, second head) alternate
+//                    first head or heads) and group B (waves 4-7) alternate
 //                    phase by phase between an MFMA phase (GEMM1 of tile t and
 //                    GEMM2 of tile t-1) and a VALU phase (softmax of tile t),
 //                    so on every SIMD one wave keeps the matrix core busy while
 //                    the other computes exponentials.  Each K/V tile staged in
-//                    LDS serves both heads.
+//                    LDS serves every head of the workgroup.
 //   attn_fwd_kernel  any D in {128, 256} and GQA ratio: 4 waves = 128 query
 //                    rows of one head; GEMM1 of tile t+1 is issued ahead of the
 //                    softmax and GEMM2 of tile t.
@@ -87,6 +88,9 @@ struct AttnParams {
   // ping-pong kernel, persistent mode: number of (long, short) query-block
   // pairs; 0 = one item per workgroup
   int pp_units;
+  // ping-pong kernel: Q heads per wave group (1: two heads x 128 query rows
+  // per item; 2: four heads x 64 rows, for GQA ratios divisible by 4)
+  int pp_hpg;
   // general kernel, causal, one round of two workgroups per CU (slot2 = the
   // CU count, > 0): workgroups bid and bid + slot2 share a CU, so the second
   // slot takes the query blocks shortest first and each CU's pair sums to
@@ -818,7 +822,11 @@ __device__ __forceinline__ void store_rows_lds(unsigned char *tile, uint16_t *ob
 }
 
 // ---------------------------------------------------------------------------
-// Ping-pong kernel: D=128, BN=64, two Q heads of a GQA group per workgroup.
+// Ping-pong kernel: D=128, BN=64, two or four Q heads of a GQA group per
+// workgroup.  With four (p.pp_hpg = 2) each item covers 64 query rows, so
+// that no wave of a causal item runs a key tile that is masked for all of its
+// rows (with 128-row items, waves holding the block's first 64 rows do at the
+// diagonal), and the staged table rows halve.
 // ---------------------------------------------------------------------------
 template <bool CAUSAL, int PRO, int ST, bool VT>
 __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
@@ -844,15 +852,21 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   const int64_t S = p.S;
 
   const int G = p.Hq / p.Hkv;
-  const int HP = G / 2;  // head pairs per KV head
+  const int hpg = p.pp_hpg;     // Q heads per wave group
+  const int BMI = BM / hpg;     // query rows per item
+  const int HP = G / (2 * hpg);  // items of one query block per KV head (head pairs or quads)
   const int npairs = p.B * p.Hkv * HP;
+  // wave's head within the item's 2*hpg heads and its 32-row block
+  const int hsub = grp * hpg + (hpg == 2 ? (wq >> 1) : 0);
+  const int rblk = hpg == 2 ? (wq & 1) : wq;
   const uint32_t lds0 = (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) unsigned char *)smem);
 
-  // One work item: query block qb of head pair j of KV head kvi.
+  // One work item: query block qb (BMI rows) of head pair (or quad) j of KV
+  // head kvi.
   auto run = [&](const int qb, const int kvi, const int j) {
   const int b = kvi / p.Hkv;
   const int kvh = kvi - b * p.Hkv;
-  const int h = kvh * G + 2 * j + grp;
+  const int h = kvh * G + 2 * hpg * j + hsub;
   const int64_t qoff = ((int64_t)b * p.Hq + h) * S;
   const int64_t kvoff = ((int64_t)b * p.Hkv + kvh) * S;
 
@@ -888,10 +902,10 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     }
   };
 
-  const int q0 = qb * BM + wq * 32;
+  const int q0 = qb * BMI + rblk * 32;
   const int qrow = q0 + lr;
   const bool qvalid = qrow < S;
-  const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BM < S ? (int64_t)(qb + 1) * BM : S) : S;
+  const int64_t kv_end = CAUSAL ? ((int64_t)(qb + 1) * BMI < S ? (int64_t)(qb + 1) * BMI : S) : S;
   const int nT = (int)((kv_end + BN - 1) / BN);
 
   copy_k(0, K0);
@@ -900,18 +914,18 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
   lds_read_offsets<D>(lane, kra, vra);
   StagedTables tab;
   if constexpr (STAGE_TAB) {
-    // wave w copies rows 16w .. 16w+15 of each table, 4 rows per copy, with
+    // wave w copies rows (BMI/8)w .. of each table, 4 rows per copy, with
     // the K tiles' chunk swizzle, so kra[c] addresses the lane's row chunk
     const i32x4_t crs = buffer_rsrc(p.cos, (uint32_t)(S * 2 * D));
     const i32x4_t srs = buffer_rsrc(p.sin, (uint32_t)(S * 2 * D));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 4 * w + i;
-      const uint32_t voff = copy_lane_offset<D>(j, lane, false) + (uint32_t)(qb * BM * 2 * D);
+    const int ncp = 4 / hpg;
+    for (int i = 0; i < ncp; ++i) {
+      const int j = ncp * w + i;
+      const uint32_t voff = copy_lane_offset<D>(j, lane, false) + (uint32_t)(qb * BMI * 2 * D);
       copy16_to_lds(crs, lds0 + TROWS + j * 1024, voff);
       copy16_to_lds(srs, lds0 + TROWS + TAB_BYTES + j * 1024, voff);
     }
-    tab.cos = smem + TROWS + wq * 32 * 2 * D;
+    tab.cos = smem + TROWS + rblk * 32 * 2 * D;
     tab.sin = tab.cos + TAB_BYTES;
     tab.off = kra;
   }
@@ -1012,7 +1026,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 
   // ---- work items.  Persistent (pp_units > 0, causal): workgroup bid takes
   // units bid, bid + grid, ...; unit u pairs query blocks R-1-m and m of one
-  // head pair, so every unit holds the same number of key tiles, and the
+  // head pair (or quad), so every unit holds the same number of key tiles, and the
   // grid (a multiple of 8) keeps unit u on XCD u % 8, the home of its KV
   // head.  Otherwise one item per workgroup, heaviest blocks first.  Both
   // share one call site of `run`, so its body is emitted once. ----
@@ -1534,6 +1548,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   AttnParams p;
   p.n_items = 0;
   p.pp_units = 0;
+  p.pp_hpg = 1;
   p.slot2 = 0;
   p.counters = nullptr;
   p.partials = nullptr;
@@ -1554,7 +1569,9 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   if (pp && a.vt && a.S % 8 == 0) p.vt = a.vt;  // V^T rows must be 16-byte aligned
   int blocks;
   if (pp) {
-    const int npairs = p.B * p.Hkv * (G / 2);
+    p.pp_hpg = G % 4 == 0 ? 2 : 1;
+    p.n_qblocks = (int)((a.S + BM / p.pp_hpg - 1) / (BM / p.pp_hpg));
+    const int npairs = p.B * p.Hkv * (G / (2 * p.pp_hpg));
     p.xcd_remap = ((p.B * p.Hkv) % 8 == 0 && npairs % 8 == 0) ? 1 : 0;
     blocks = p.n_qblocks * npairs;
     // persistent mode when the (long, short) pairs fill every CU equally
