@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 6
+#define KFMI_ABI_VERSION 7
 
 /* status codes */
 #define KFMI_OK 0
@@ -53,6 +53,12 @@ extern "C" {
 #define KFMI_MODE_QUERY 0   /* K prepared once, Q norm(+RoPE) in the attention prologue */
 #define KFMI_MODE_UNFUSED 1 /* Q and K prepared, plain attention */
 #define KFMI_MODE_FULL 2    /* one launch: Q and K norm(+RoPE) inside attention, K per key tile */
+
+/* attention kernels (kfmi_tuning.attn_kernel, kfmi_launch_info.kernel) */
+#define KFMI_KERNEL_AUTO 0     /* chosen by shape */
+#define KFMI_KERNEL_GENERAL 1  /* attn_fwd_kernel: 4 waves x 32 rows of one head, D 128 or 256 */
+#define KFMI_KERNEL_PINGPONG 2 /* attn_pp_kernel: 8 waves, two wave groups alternating MFMA and softmax phases */
+#define KFMI_KERNEL_WIDE 3     /* attn_ww_kernel: 4 waves x 64 rows, four heads of a GQA group per item */
 
 /* Version of this ABI (KFMI_ABI_VERSION). */
 int kfmi_abi_version(void);
@@ -78,6 +84,33 @@ typedef struct {
  * launch_factored_attention qk:651), whose consumer reads registers, spills
  * and shared memory (fusion_harness.py:82-102 compiler_evidence). */
 int kfmi_last_launches(kfmi_launch_info *out, int max);
+
+/* Dispatch choices that the library otherwise makes by shape, for tuning
+ * runs: the counterpart of the Triton tile arguments (bm, bn, warps, stages,
+ * gather) that the reference's tuning runner sweeps (tune_refinement,
+ * rope:765-814).  Settings apply to later calls of the calling thread only;
+ * a field left at 0 keeps the shape-based choice.  A forced choice that
+ * cannot run a call's shape makes that call fail with KFMI_EINVAL before
+ * anything is launched.  Results never depend on these settings beyond
+ * last-bit differences of the kernels' own summation orders. */
+typedef struct {
+  int32_t attn_kernel; /* KFMI_KERNEL_*; modes other than FULL (FULL always runs the general kernel) */
+  int32_t pp_heads;    /* ping-pong kernel: Q heads per wave group, 1 (two heads x 128 rows per
+                          item) or 2 (four heads x 64 rows; GQA ratio a multiple of 4) */
+  int32_t rows_heads;  /* preparation kernel: heads per workgroup for Q+K launches at D = 128,
+                          2 or 4 (4 only without V^T and outside the factored preparation) */
+  int32_t split;       /* general kernel at D = 256: 1 never splits a query block's key range */
+  int32_t persistent;  /* ping-pong and wide kernels: 1 = one work item per workgroup (no
+                          persistent long/short pairing) */
+} kfmi_tuning;
+
+/* Set (t != NULL) or clear (t == NULL) the calling thread's overrides.
+ * Returns KFMI_EINVAL for out-of-range fields.  No counterpart in the
+ * reference (see kfmi_tuning). */
+int kfmi_set_tuning(const kfmi_tuning *t);
+
+/* The calling thread's current overrides (all zero unless set). */
+void kfmi_get_tuning(kfmi_tuning *out);
 
 /* Row preparation: per-(token,head) RMSNorm(eps) * gamma, then optional
  * rotate-half RoPE, BF16 out.  Replaces prepare_attention -> prepare_kernel

@@ -14,12 +14,15 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
 PREP_ONLY_K, PREP_ROPE = 1, 2
 MODE_QUERY, MODE_UNFUSED, MODE_FULL = 0, 1, 2
+# attention kernels (KFMI_KERNEL_*)
+KERNEL_AUTO, KERNEL_GENERAL, KERNEL_PINGPONG, KERNEL_WIDE = 0, 1, 2, 3
+KERNELS = {"auto": KERNEL_AUTO, "general": KERNEL_GENERAL, "pingpong": KERNEL_PINGPONG, "wide": KERNEL_WIDE}
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -72,6 +75,10 @@ def load() -> ctypes.CDLL:
         lib.kfmi_attention_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I]
         lib.kfmi_last_launches.restype = ctypes.c_int
         lib.kfmi_last_launches.argtypes = [ctypes.POINTER(LaunchInfo), _I]
+        lib.kfmi_set_tuning.restype = ctypes.c_int
+        lib.kfmi_set_tuning.argtypes = [ctypes.POINTER(Tuning)]
+        lib.kfmi_get_tuning.restype = None
+        lib.kfmi_get_tuning.argtypes = [ctypes.POINTER(Tuning)]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
@@ -86,6 +93,57 @@ class LaunchInfo(ctypes.Structure):
     """kfmi_launch_info of include/kfmi.h."""
     _fields_ = [("kernel", ctypes.c_char * 96), ("grid", ctypes.c_int64), ("block", ctypes.c_int32),
                 ("registers", ctypes.c_int32), ("lds_bytes", ctypes.c_int32), ("scratch_bytes", ctypes.c_int32)]
+
+
+class Tuning(ctypes.Structure):
+    """kfmi_tuning of include/kfmi.h: dispatch choices the library otherwise
+    makes by shape (0 = by shape)."""
+    _fields_ = [("attn_kernel", ctypes.c_int32), ("pp_heads", ctypes.c_int32), ("rows_heads", ctypes.c_int32),
+                ("split", ctypes.c_int32), ("persistent", ctypes.c_int32)]
+
+
+TUNING_FIELDS = tuple(f for f, _ in Tuning._fields_)
+
+
+def get_tuning() -> dict:
+    """The calling thread's dispatch overrides (kfmi_get_tuning)."""
+    t = Tuning()
+    load().kfmi_get_tuning(ctypes.byref(t))
+    return {f: getattr(t, f) for f in TUNING_FIELDS}
+
+
+def set_tuning(**fields) -> None:
+    """Set the calling thread's dispatch overrides (kfmi_set_tuning); fields
+    not given are 0 (by shape).  ``attn_kernel`` also takes a name of
+    KERNELS.  For tuning runs and tests: the reference-signature ops never
+    call this."""
+    unknown = set(fields) - set(TUNING_FIELDS)
+    if unknown:
+        raise ValueError(f"unknown tuning fields {sorted(unknown)}")
+    if isinstance(fields.get("attn_kernel"), str):
+        fields["attn_kernel"] = KERNELS[fields["attn_kernel"]]
+    t = Tuning(**{f: int(fields.get(f, 0)) for f in TUNING_FIELDS})
+    lib = load()
+    if lib.kfmi_set_tuning(ctypes.byref(t)) != KFMI_OK:
+        raise ValueError(f"kfmi_set_tuning: {lib.kfmi_last_error().decode(errors='replace')}")
+
+
+class tuning:
+    """``with tuning(attn_kernel='wide'): ...`` -- overrides for the block,
+    then the previous ones again."""
+
+    def __init__(self, **fields):
+        self.fields = fields
+        self.saved: dict | None = None
+
+    def __enter__(self):
+        self.saved = get_tuning()
+        set_tuning(**self.fields)
+        return self
+
+    def __exit__(self, *exc):
+        set_tuning(**self.saved)
+        return False
 
 
 def last_launches(max_records: int = 8) -> list[dict]:

@@ -29,10 +29,11 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", str(INCL
           "-Wall", "-Wno-unused-function"]
 
 
-# Per-file flags.  attention.hip: no NaN inputs reach its max reductions
+# Per-file flags.  The attention kernels: no NaN inputs reach their max reductions
 # (masked scores are -inf, not NaN), and without NaN semantics fmaxf needs no
 # canonicalising instructions, so max trees map onto v_max3_f32.
-FILE_FLAGS = {"attention.hip": ["-fno-honor-nans"]}
+_NO_NANS = ["-fno-honor-nans"]
+FILE_FLAGS = {"attention.hip": _NO_NANS, "attn_pp.hip": _NO_NANS, "attn_wide.hip": _NO_NANS}
 
 
 def hipcc() -> str:

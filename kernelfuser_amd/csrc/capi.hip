@@ -19,6 +19,7 @@ namespace {
 
 thread_local std::string g_error;
 thread_local std::vector<kfmi_launch_info> g_launches;
+thread_local kfmi_tuning g_tuning{};
 
 int fail(int code, const char *fmt, ...) {
   char buf[512];
@@ -40,6 +41,8 @@ int launch_status(hipError_t e, const char *what) {
 }  // namespace
 
 namespace kfmi {
+
+const kfmi_tuning &thread_tuning() { return g_tuning; }
 
 void launch_log_clear() { g_launches.clear(); }
 
@@ -146,6 +149,28 @@ int kfmi_abi_version(void) { return KFMI_ABI_VERSION; }
 
 const char *kfmi_last_error(void) { return g_error.c_str(); }
 
+int kfmi_set_tuning(const kfmi_tuning *t) {
+  if (t == nullptr) {
+    g_tuning = kfmi_tuning{};
+    g_error.clear();
+    return KFMI_OK;
+  }
+  if (t->attn_kernel < KFMI_KERNEL_AUTO || t->attn_kernel > KFMI_KERNEL_WIDE)
+    return fail(KFMI_EINVAL, "attn_kernel must be KFMI_KERNEL_AUTO .. KFMI_KERNEL_WIDE (got %d)", t->attn_kernel);
+  if (t->pp_heads < 0 || t->pp_heads > 2) return fail(KFMI_EINVAL, "pp_heads must be 0, 1 or 2 (got %d)", t->pp_heads);
+  if (t->rows_heads != 0 && t->rows_heads != 2 && t->rows_heads != 4)
+    return fail(KFMI_EINVAL, "rows_heads must be 0, 2 or 4 (got %d)", t->rows_heads);
+  if (t->split < 0 || t->split > 1) return fail(KFMI_EINVAL, "split must be 0 or 1 (got %d)", t->split);
+  if (t->persistent < 0 || t->persistent > 1) return fail(KFMI_EINVAL, "persistent must be 0 or 1 (got %d)", t->persistent);
+  g_tuning = *t;
+  g_error.clear();
+  return KFMI_OK;
+}
+
+void kfmi_get_tuning(kfmi_tuning *out) {
+  if (out) *out = g_tuning;
+}
+
 int kfmi_last_launches(kfmi_launch_info *out, int max) {
   const int n = (int)g_launches.size();
   for (int i = 0; i < n && i < max && out; ++i) out[i] = g_launches[i];
@@ -176,6 +201,12 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *g
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.S = S; a.D = D;
   a.only_k = only_k; a.rope = rope; a.style = style_of(norm_style); a.eps = eps;
   return launch_status(kfmi::launch_rows(a, (hipStream_t)stream), "prepare launch");
+}
+
+// The thread's dispatch overrides must be able to run this shape.
+static int check_tuning(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full) {
+  const char *why = kfmi::attention_tuning_error(Hq, Hkv, S, D, full);
+  return why ? fail(KFMI_EINVAL, "kfmi_set_tuning: %s", why) : KFMI_OK;
 }
 
 static int attention_impl(const void *q, const void *k, const void *v, const void *vt, const void *gq,
@@ -220,6 +251,7 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
   if (fuse_q && cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_work(work, work_bytes));
+  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
   KFMI_TRY(check_device());
   const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
@@ -251,6 +283,7 @@ static int launch_attention_entry(const void *q, const void *k, const void *v, c
   if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
   if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
+  KFMI_TRY(check_tuning(Hq, Hkv, S, D, mode == KFMI_MODE_FULL));
   KFMI_TRY(check_device());
   int64_t clear_bytes = 0;
   if (noalloc) {
@@ -281,7 +314,7 @@ static int launch_attention_entry(const void *q, const void *k, const void *v, c
   }
   const bool rope = cos != nullptr;
   // V^T is used by the ping-pong kernel when its rows are 16-byte aligned.
-  const bool use_vt = vt != nullptr && kfmi::attention_uses_pp(Hq, Hkv, S, D) && S % 8 == 0;
+  const bool use_vt = vt != nullptr && kfmi::attention_kernel(Hq, Hkv, S, D, false) == KFMI_KERNEL_PINGPONG && S % 8 == 0;
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
   r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;
@@ -351,6 +384,7 @@ int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, f
   if (inv_mode != 0 && inv_mode != 1) return fail(KFMI_EINVAL, "inv_mode must be 0 (read) or 1 (compute)");
   if (inv_mode == 0) KFMI_TRY(check_ptrs({{inv, "inv"}}));
   if (inv && (reinterpret_cast<uintptr_t>(inv) & 3u)) return fail(KFMI_EINVAL, "inv must be 4-byte aligned");
+  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
   KFMI_TRY(check_device());
   const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
   return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
@@ -364,6 +398,7 @@ int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void
   KFMI_TRY(check_tiles(bm, bn));
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}, {inv, "inv"}, {kn, "kn"}}));
   if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
+  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
   KFMI_TRY(check_device());
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;

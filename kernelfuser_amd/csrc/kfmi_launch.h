@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kfmi.h"
+
 namespace kfmi {
 
 // Row styles of the preparation and attention-prologue arithmetic.
@@ -63,9 +65,14 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
 // vt[b,h,d,s] = v[b,h,s,d] for the B*H heads of S rows of D.
 hipError_t launch_transpose_v(const uint16_t *v, uint16_t *vt, int64_t BH, int64_t S, int64_t D, hipStream_t stream);
 hipError_t launch_attention(const AttnArgs &a, hipStream_t stream);
-// Whether launch_attention runs the ping-pong kernel (the one that reads V^T)
-// for this shape (modes other than 'full').
-bool attention_uses_pp(int64_t Hq, int64_t Hkv, int64_t S, int64_t D);
+// The calling thread's dispatch overrides (kfmi_set_tuning; all zero unless set).
+const kfmi_tuning &thread_tuning();
+// The attention kernel (KFMI_KERNEL_GENERAL / _PINGPONG / _WIDE) that
+// launch_attention runs for this shape under the thread's overrides; `full`
+// is mode 'full' (always the general kernel).
+int attention_kernel(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full);
+// Why the thread's overrides cannot run this shape (NULL: they can).
+const char *attention_tuning_error(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full);
 // Workspace bytes with which launch_attention splits the key range of the
 // longest causal query blocks over two workgroups (0: this shape never splits).
 int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal);

@@ -344,8 +344,10 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   const int64_t rpb = 256 / (a.D / 8);
   p.nblk = (uint32_t)((a.S + rpb - 1) / rpb);
   const int64_t rows = (int64_t)(p.heads_q + p.heads_k) * a.S;
-  p.hpw = (a.D == 128 && !a.only_k && !a.vt && a.style != ST_FACTORED && rows >= ROWS_BIG &&
-            a.S <= ROWS_BIG_MAX_S) ? ROWS_HPW_BIG : ROWS_HPW;
+  const bool big_ok = a.D == 128 && !a.only_k && !a.vt && a.style != ST_FACTORED;  // where the 4-head form exists
+  const int forced = thread_tuning().rows_heads;
+  p.hpw = big_ok && (forced ? forced == ROWS_HPW_BIG : rows >= ROWS_BIG && a.S <= ROWS_BIG_MAX_S) ? ROWS_HPW_BIG
+                                                                                                   : ROWS_HPW;
   const int64_t units = (p.heads_q + p.hpw - 1) / p.hpw + (p.heads_k + p.hpw - 1) / p.hpw;
   p.row_blocks = (uint32_t)(units * p.nblk);
   p.vt_sblocks = (int)((a.S + 63) / 64);

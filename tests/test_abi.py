@@ -26,7 +26,8 @@ def lib():
 
 def test_header_declares_the_bound_entry_points():
     names = _declared()
-    queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes", "kfmi_last_launches"}
+    queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes", "kfmi_last_launches",
+               "kfmi_set_tuning", "kfmi_get_tuning"}
     assert queries <= set(names)
     assert set(_lib.SIGNATURES) == set(names) - queries
 
@@ -147,3 +148,30 @@ def test_failed_call_reports_no_launches(lib):
     lib.kfmi_transpose_v_bf16(P, P, 4, 100, 128, None)  # rejected before any launch
     assert lib.kfmi_last_launches(None, 0) == 0
     assert _lib.last_launches() == []
+
+
+def test_tuning_overrides_validate_and_scope(lib):
+    """kfmi_set_tuning rejects out-of-range fields, keeps settings per
+    thread, and a forced kernel that cannot run a shape fails the call with
+    KFMI_EINVAL before any device access."""
+    assert _lib.get_tuning() == dict.fromkeys(_lib.TUNING_FIELDS, 0)
+    for bad in ({"attn_kernel": 4}, {"pp_heads": 3}, {"rows_heads": 1}, {"split": 2}, {"persistent": -1}):
+        with pytest.raises(ValueError):
+            _lib.set_tuning(**bad)
+    assert _lib.get_tuning() == dict.fromkeys(_lib.TUNING_FIELDS, 0)
+    args = (P, P, P, None, P, P, P, P, 1, 16, 8, 4096, 128, 0.1, 1e-6, 1, 1, 2, 128, 64, None, 0, None)
+    with _lib.tuning(attn_kernel="wide"):
+        assert lib.kfmi_attention_bf16(*args) == EINVAL  # GQA ratio 2
+        assert "wide kernel" in _err(lib)
+        import threading
+        seen = {}
+        th = threading.Thread(target=lambda: seen.update(_lib.get_tuning()))
+        th.start()
+        th.join()
+        assert seen["attn_kernel"] == 0  # another thread keeps its own settings
+    with _lib.tuning(attn_kernel="pingpong", pp_heads=2):
+        assert lib.kfmi_attention_bf16(*args) == EINVAL  # four heads per item need a ratio of 4
+    args256 = args[:12] + (256,) + args[13:]
+    with _lib.tuning(attn_kernel="pingpong"):
+        assert lib.kfmi_attention_bf16(*args256) == EINVAL
+    assert _lib.get_tuning()["attn_kernel"] == 0
