@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+from collections.abc import Sequence
 from pathlib import Path
 
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
@@ -158,11 +159,85 @@ def last_launches(max_records: int = 8) -> list[dict]:
             for r in buf[:min(n, max_records)]]
 
 
+_tls = threading.local()
+
+
+def _calls() -> int:
+    """Successful compute calls made by this thread so far."""
+    return getattr(_tls, "calls", 0)
+
+
+class Launches(Sequence):
+    """The kernels one compute call launched, read from the library only when
+    first used (so an eager launch costs one ctypes call).  The library keeps
+    the records of a thread's last call only: reading a handle after a later
+    call on the same thread raises instead of returning that call's kernels."""
+
+    def __init__(self):
+        self._thread = threading.get_ident()
+        self._call = _calls()
+        self._records = None
+
+    def _get(self) -> list:
+        if self._records is None:
+            if threading.get_ident() != self._thread or _calls() != self._call:
+                raise RuntimeError("launch records are read before the next compute call of the same thread")
+            self._records = last_launches()
+        return self._records
+
+    def __getitem__(self, i):
+        return self._get()[i]
+
+    def __len__(self) -> int:
+        return len(self._get())
+
+    def __eq__(self, other) -> bool:
+        return list(self._get()) == list(other)
+
+    def __repr__(self) -> str:
+        return f"Launches({self._get()!r})"
+
+
+class record_launches:
+    """``with record_launches() as rec: ...`` -- collects the launch records of
+    every compute call the block makes on this thread into ``rec.launches``
+    (the runners' per-arm kernel evidence).  Nests; each level sees its own
+    block's calls."""
+
+    def __init__(self):
+        self.launches: list[dict] = []
+
+    def __enter__(self):
+        stack = getattr(_tls, "recorders", None)
+        if stack is None:
+            stack = _tls.recorders = []
+        stack.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        _tls.recorders.remove(self)
+        return False
+
+    def kernels(self) -> list[str]:
+        """The distinct kernel instances, in first-launch order."""
+        seen = []
+        for r in self.launches:
+            if r["kernel"] not in seen:
+                seen.append(r["kernel"])
+        return seen
+
+
 def call(name: str, *args) -> None:
     """Call a compute entry point; map its status to ValueError / KfmiError."""
     lib = load()
     rc = getattr(lib, name)(*args)
     if rc == KFMI_OK:
+        _tls.calls = _calls() + 1
+        recs = getattr(_tls, "recorders", None)
+        if recs:
+            got = last_launches()
+            for r in recs:
+                r.launches.extend(got)
         return
     msg = lib.kfmi_last_error().decode(errors="replace")
     if rc == KFMI_EINVAL:

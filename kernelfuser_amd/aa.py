@@ -32,7 +32,7 @@ from pathlib import Path
 
 import torch
 
-from . import exclusive, timing
+from . import _lib, exclusive, timing
 from .inputs import QWEN3_8B, make_inputs
 
 DEFAULT_ROUNDS, DEFAULT_SAMPLES, DEFAULT_LAUNCHES = 5, 40, 20
@@ -92,10 +92,21 @@ def run_row(b: int, s: int, rounds: int = DEFAULT_ROUNDS, samples: int = DEFAULT
         for label, order_seed in (("initial", seed), ("retest", seed + 104729)):
             xa, xb = host.to(device).astuple(), host.to(device).astuple()  # separate copies per pass
             arm = lambda xs: (lambda: optimized_attention(*xs, causal=True, mode=mode, norm_style=norm_style))
-            ea, eb = arm(xa)(), arm(xb)()
+            with _lib.record_launches() as ka:
+                ea = arm(xa)()
+            with _lib.record_launches() as kb:
+                eb = arm(xb)()
             eager = bitwise(ea, eb)
             if not eager["pass"]:
                 raise RuntimeError(f"eager A1/A2 outputs differ or are not finite: {eager}")
+            # each arm's kernels of this library (the reference keeps a kernel
+            # trace per arm, e7_rope_aa.py:89-113); an arm without any measured
+            # something else
+            eager["kernels"] = {"A1": ka.launches, "A2": kb.launches}
+            if not ka.launches or not kb.launches:
+                row["status"] = "invalid_no_kernel"
+                row[label] = {"eager_check": eager}
+                return row
             rec = aa_pass(arm(xa), arm(xb), ea, rounds=rounds, samples=samples, launches=launches,
                           seed=order_seed)
             rec["eager_check"] = eager

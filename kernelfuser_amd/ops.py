@@ -144,8 +144,8 @@ def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_nor
     ``rope=False`` the table entries are ignored.  ``rows`` (Triton rows per
     program) is ignored.  ``vt`` (optional, D=128, S % 8 == 0): the same launch
     also writes V transposed per head into it (the V^T operand of
-    ``attention_prefill``).  Returns the launched kernel's record
-    (``_lib.last_launches``), where the reference returns its kernel object.
+    ``attention_prefill``).  Returns the launched kernel's record (a lazy
+    ``_lib.Launches``), where the reference returns its kernel object.
     """
     q, k, v, gq, gk, cos, sin = inputs
     b, h, s, d = q.shape
@@ -156,7 +156,7 @@ def prepare_attention(inputs, qn, kn, *, only_k=False, rows=4, rope=True, hf_nor
               ptr(cos) if rope else None, ptr(sin) if rope else None,
               None if only_k else ptr(qn), ptr(kn), ptr(vt),
               b, h, k.shape[1], s, d, float(eps), _style(norm_style, hf_norm), flags, stream_of(k))
-    return _lib.last_launches()
+    return _lib.Launches()
 
 
 def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, warps=4, stages=1,
@@ -184,8 +184,10 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
     ``attention_workspace_bytes`` bytes); ``None`` uses a cached one per device.
 
     Returns the launched kernels (``kfmi_last_launches``: instance, grid, block,
-    registers, LDS and scratch per kernel), where the reference returns its
-    attention kernel object (rope:674-677).
+    registers, LDS and scratch per kernel) as a lazy ``_lib.Launches``, read
+    from the library on first use and valid until the thread's next compute
+    call, where the reference returns its attention kernel object
+    (rope:674-677).
     """
     if mode not in ("full", "query", "unfused"):
         raise ValueError("Invalid fusion mode")
@@ -201,7 +203,7 @@ def launch_attention(inputs, out, *, causal=False, mode="query", bm=64, bn=64, w
               b, h, k.shape[1], s, d, float(d) ** -0.5, EPS, int(bool(causal)),
               {"query": MODE_QUERY, "unfused": MODE_UNFUSED, "full": MODE_FULL}[mode], _style(norm_style, hf_norm),
               _bm(bm), _bn(bn), wp, wb, stream_of(q))
-    return _lib.last_launches()
+    return _lib.Launches()
 
 
 def attention_prefill(q, kn, v, out, *, gq=None, cos=None, sin=None, causal=False, fuse_q=True,
@@ -239,7 +241,7 @@ def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=6
     _lib.call("kfmi_launch_factored_attention_bf16",
               ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk), ptr(out), ptr(inv), ptr(kn),
               b, h, k.shape[1], s, d, EPS, int(bool(causal)), _bm(bm), _bn(bn), stream_of(q))
-    return _lib.last_launches()
+    return _lib.Launches()
 
 
 def prepare_factored(inputs, inv, kn):

@@ -43,6 +43,8 @@ from pathlib import Path
 import torch
 import torch.nn.functional as F
 
+from . import _lib
+
 ATOL = 2.5e-2
 RTOL = 2.5e-2
 TOP1_MIN = 0.999
@@ -270,8 +272,16 @@ def run_row(model, b: int, s: int, *, samples: int = 10, rounds: int = 3, timing
         restore(saved)
     saved = patch(model, "fused")
     try:
-        got = forward_logits(model, ids)
+        with _lib.record_launches() as kern:
+            got = forward_logits(model, ids)
         row["correctness"] = quality(got, ref, ids)
+        # the candidate's kernels of this library (two launches per layer);
+        # a forward that launched none did not run the fused path
+        row["candidate_kernels"] = kern.kernels()
+        row["candidate_launches"] = len(kern.launches)
+        if not kern.launches:
+            row["status"] = "invalid_no_kernel"
+            return row
         row["correctness"]["pass_noise_floor"] = noise_floor_gate(row["correctness"], row["noise_floor"])
         if row["correctness"]["pass"]:
             row["status"] = "pass"

@@ -27,6 +27,12 @@ Counterpart of the reference's ``verify_refinement``
    vendor arm (5 rounds x 7 samples, another order seed);
 4. gates the selected arms again on two more input seeds (2909, 3909).
 
+Every arm's gate record also lists the kernels of this library it launched
+(``kfmi_last_launches`` records: instance, grid, block, registers, LDS,
+scratch), the counterpart of the reference's per-arm kernel trace
+(rope:344-351); a row in which a passing arm launched none is marked
+``invalid_no_kernel`` and not timed.
+
 Tail checks (S = 33, 129; causal and not; every mode) follow the grid, as at
 rope:895-908 and qk:718-730.
 
@@ -48,7 +54,7 @@ from pathlib import Path
 
 import torch
 
-from . import exclusive, timing
+from . import _lib, exclusive, timing
 from .inputs import make_inputs
 from .ops import MODELS, launch_attention, launch_factored_attention, prepare_attention
 
@@ -191,17 +197,30 @@ FUSED = ("query", "full", "factored")
 
 
 def check_arms(arms, ref):
-    """Run every arm once and gate it; failing arms are removed from ``arms``."""
+    """Run every arm once and gate it; failing arms are removed from ``arms``.
+    Each check also records the kernels of this library the arm launched
+    (instance, grid, block, registers, LDS, scratch): the counterpart of the
+    reference's per-arm kernel trace (rope:344-351)."""
     checks = {}
     for name, call in list(arms.items()):
         try:
-            checks[name] = gate(call(), ref)
+            with _lib.record_launches() as rec:
+                out = call()
+            checks[name] = gate(out, ref)
+            checks[name]["kernels"] = rec.launches
             torch.cuda.synchronize()
         except Exception as exc:  # an arm PyTorch cannot run, or an argument the library refuses
             checks[name] = {"pass": False, "error": repr(exc)}
         if not checks[name]["pass"]:
             del arms[name]
     return checks
+
+
+def without_kernel_evidence(checks) -> list:
+    """Passing arms that launched no kernel of this library (every arm here,
+    the vendor one included through its preparation launch, must launch one;
+    one that did not measured something else)."""
+    return [n for n, c in checks.items() if c.get("pass") and not c.get("kernels")]
 
 
 def run_row(model: str, b: int, s: int, causal: bool, rotary: bool, *, rounds=(3, 5), samples=(5, 7),
@@ -214,6 +233,11 @@ def run_row(model: str, b: int, s: int, causal: bool, rotary: bool, *, rounds=(3
     del ref
     row = {"model": model, "shape": [b, s, causal], "rotary": rotary, "geometry": list(MODELS[model]),
            "correctness": checks}
+    missing = without_kernel_evidence(checks)
+    if missing:
+        row["status"] = "invalid_no_kernel"
+        row["arms_without_kernels"] = missing
+        return row
     fused = [n for n in arms if n in FUSED]
     if not fused or "unfused" not in arms:
         row["status"] = "failed_gate"

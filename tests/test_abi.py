@@ -175,3 +175,18 @@ def test_tuning_overrides_validate_and_scope(lib):
     with _lib.tuning(attn_kernel="pingpong"):
         assert lib.kfmi_attention_bf16(*args256) == EINVAL
     assert _lib.get_tuning()["attn_kernel"] == 0
+
+
+def test_launch_handle_reads_only_its_own_call():
+    """A launcher's lazy record handle is valid until the thread's next
+    compute call; a read after it raises (no GPU call is made here)."""
+    h = _lib.Launches()
+    assert list(h) == [] and len(h) == 0  # this thread's last call launched nothing
+    stale = _lib.Launches()
+    _lib._tls.calls = _lib._calls() + 1  # as a later successful call would
+    with pytest.raises(RuntimeError):
+        len(stale)
+    with _lib.record_launches() as outer:
+        with _lib.record_launches() as inner:
+            pass
+    assert outer.launches == [] and inner.kernels() == []

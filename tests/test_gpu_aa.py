@@ -18,6 +18,9 @@ def test_aa_row_short(gpu):
     for key in ("initial", "retest"):
         rec = row[key]
         assert rec["eager_check"]["pass"]
+        kern = rec["eager_check"]["kernels"]
+        assert [r["kernel"].split("<")[0] for r in kern["A1"]] == ["rows_kernel", "attn_fwd_kernel"]
+        assert [r["kernel"] for r in kern["A1"]] == [r["kernel"] for r in kern["A2"]]
         assert len(rec["replay_checks"]) == 2 and all(c["pass"] for c in rec["replay_checks"])
         assert rec["A1"]["n"] == 4 and rec["A2"]["n"] == 4
         assert math.isfinite(rec["paired_ratio_median"]) and 0.5 < rec["paired_ratio_median"] < 2.0

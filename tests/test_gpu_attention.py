@@ -333,3 +333,24 @@ def test_launchers_return_their_kernels(gpu):
                                   torch.empty_like(fx.k), causal=True)
     torch.cuda.synchronize()
     assert [r["kernel"].split("<")[0] for r in f] == ["rows_kernel", "attn_fwd_kernel"]
+
+
+def test_launch_records_are_lazy_and_scoped(gpu):
+    """The launchers' records are read from the library on first use; a handle
+    read after a later call of the same thread raises rather than returning
+    that call's kernels, and record_launches collects every call of a block."""
+    from kernelfuser_amd import _lib, prepare_attention
+    xs = make_inputs(1, 256, QWEN3_8B, 33).to(gpu)
+    out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
+    announce("lazy launch records B=1 S=256")
+    with _lib.record_launches() as rec:
+        first = launch_attention(xs.reference7, out, causal=True, mode="query", kn=kn, norm_style="fp32")
+        assert len(first) == 2 and first[1]["kernel"].startswith("attn_fwd_kernel")
+        stale = prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+        prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
+        with pytest.raises(RuntimeError):
+            len(stale)
+    torch.cuda.synchronize()
+    assert [r["kernel"].split("<")[0] for r in rec.launches] == ["rows_kernel", "attn_fwd_kernel", "rows_kernel",
+                                                                 "rows_kernel"]
+    assert list(first) == rec.launches[:2]  # read before the next call, kept since

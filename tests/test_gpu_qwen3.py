@@ -27,6 +27,9 @@ def test_qwen3_prefill_gates(model, b, s):
     assert row["status"] in ("pass", "pass_noise_floor"), (row["correctness"], row["noise_floor"])
     m = row["correctness"]
     assert m["pass_noise_floor"] and m["nll_abs_diff"] <= 2.5e-2 and m["relative_l2"] <= 2.5e-2
+    # the candidate ran this library's kernels: two launches per attention layer
+    assert row["candidate_launches"] == 2 * 2
+    assert [k.split("<")[0] for k in row["candidate_kernels"]] == ["rows_kernel", "attn_fwd_kernel"]
     if b == 1:
         # timed against the vendor baseline (the unpatched HF attention, BF16
         # SDPA on its fused kernels), which is itself gated on the noise floor

@@ -1,6 +1,7 @@
 """Refinement runner end to end on the GPU (one short row of each kind): every
-arm of this package passes the reference gate, the selection and the retest
-run, extra seeds pass, and the tail checks pass for every mode."""
+arm of this package passes the reference gate and records the kernels it
+launched, the selection and the retest run, extra seeds pass, and the tail
+checks pass for every mode."""
 import pytest
 
 from helpers import announce
@@ -23,6 +24,13 @@ def test_refine_row(gpu, model, b, s, causal, rotary):
     assert len(row["additional_seed_checks"]) == 4
     v = row["correctness"]["vendor_unfused"]
     assert v["pass"] or "error" in v  # unavailable on this PyTorch build is recorded, not hidden
+    # per-arm kernel evidence (the reference's per-arm trace, rope:344-351)
+    kern = {n: [r["kernel"].split("<")[0] for r in c["kernels"]] for n, c in row["correctness"].items() if c["pass"]}
+    assert kern["query"] == ["rows_kernel", "attn_fwd_kernel"] and kern["unfused"] == ["rows_kernel", "attn_fwd_kernel"]
+    assert kern["full"] == ["attn_fwd_kernel"]
+    if "vendor_unfused" in kern:
+        assert kern["vendor_unfused"] == ["rows_kernel"]
+    assert all(r["grid"] > 0 and r["registers"] > 0 for c in row["correctness"].values() for r in c.get("kernels", []))
 
 
 def test_refine_tails(gpu):
