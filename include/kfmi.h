@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 7
+#define KFMI_ABI_VERSION 8
 
 /* status codes */
 #define KFMI_OK 0
@@ -74,6 +74,10 @@ typedef struct {
   int32_t registers;     /* registers per thread (hipFuncGetAttributes numRegs) */
   int32_t lds_bytes;     /* static LDS per workgroup */
   int32_t scratch_bytes; /* private memory per thread (register spills) */
+  char plan[64];         /* choices made at launch time, "key=value" separated by spaces:
+                            attention: "hpg=<Q heads per wave group> persistent=<0|1> xcd=<0|1>"
+                            (ping-pong, wide) or "split=<query blocks split in two> pair=<0|1>
+                            xcd=<0|1>" (general); rows: "hpw=<heads per workgroup>" */
 } kfmi_launch_info;
 
 /* The kernels launched by this thread's last successful compute call, in
@@ -159,6 +163,14 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
  * whose launches never split a query block. */
 int64_t kfmi_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int causal);
 
+/* The attention kernel (KFMI_KERNEL_GENERAL, _PINGPONG or _WIDE) that an
+ * attention call of this shape and mode (KFMI_MODE_*) launches on the
+ * current device under the calling thread's overrides (kfmi_set_tuning);
+ * -KFMI_EINVAL for an invalid shape or mode, or overrides that cannot run
+ * it.  Launches nothing.  No counterpart in the reference, whose launchers
+ * always run their one Triton kernel. */
+int kfmi_attention_kernel(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int causal, int mode);
+
 /* The launches of launch_attention (rope:661-677): mode QUERY prepares K
  * into kn (K rows only) then runs attention with the fused Q prologue; mode
  * UNFUSED prepares Q into qn and K into kn, then runs plain attention; mode
@@ -168,8 +180,8 @@ int64_t kfmi_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64
  * (and qn for UNFUSED) is caller-allocated, as the reference requires
  * (rope:665-672).  cos/sin NULL disables RoPE.
  * vt (optional, may be NULL): caller-allocated scratch of V's size; when
- * given and D == 128, Hq/Hkv is even, S > 2944 (the shapes that run the
- * ping-pong kernel) and S % 8 == 0, the preparation launch
+ * given, the shape runs the ping-pong kernel (kfmi_attention_kernel) and
+ * S % 8 == 0, the preparation launch
  * also writes V transposed per head ([B,Hkv,D,S]) and the attention kernel
  * reads that instead of V (one 16-byte LDS read per V operand instead of two
  * transposing 8-byte reads).  Results are identical either way; the call
@@ -189,13 +201,15 @@ int kfmi_launch_attention_bf16(const void *q, const void *k, const void *v,
  * split-KV workspace of the causal D = 256 shapes that split (see
  * kfmi_attention_workspace_bytes) is a static device array of 36 MiB per GPU
  * (held by each GPU the library runs on until the process ends); a shape
- * whose split plan needs more returns KFMI_EINVAL before anything is
- * launched.  The call allocates nothing: when the shape splits it enqueues a
+ * whose split plan needs more runs unsplit, exactly as
+ * kfmi_launch_attention_bf16 with no workspace (results within a few ulp of
+ * the split launch's).  The call allocates nothing: when the shape splits it enqueues a
  * small fill kernel that zeroes the plan's arrival counters ahead of the
  * other launches.  Every call on one GPU shares that GPU's array, so calls
  * that overlap in time on one GPU (several streams, or concurrent graph
  * replays) race on it.  Results are identical to kfmi_launch_attention_bf16
- * with a zero-filled caller workspace. */
+ * with a zero-filled caller workspace (with none, for the plans that do not
+ * fit). */
 int kfmi_launch_attention_bf16_noalloc(const void *q, const void *k, const void *v,
                                        const void *gq, const void *gk, const void *cos,
                                        const void *sin, void *out, void *qn, void *kn, void *vt,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -74,6 +74,8 @@ def load() -> ctypes.CDLL:
         lib.kfmi_last_error.argtypes = []
         lib.kfmi_attention_workspace_bytes.restype = ctypes.c_int64
         lib.kfmi_attention_workspace_bytes.argtypes = [_I64, _I64, _I64, _I64, _I64, _I]
+        lib.kfmi_attention_kernel.restype = ctypes.c_int
+        lib.kfmi_attention_kernel.argtypes = [_I64, _I64, _I64, _I64, _I64, _I, _I]
         lib.kfmi_last_launches.restype = ctypes.c_int
         lib.kfmi_last_launches.argtypes = [ctypes.POINTER(LaunchInfo), _I]
         lib.kfmi_set_tuning.restype = ctypes.c_int
@@ -93,7 +95,19 @@ def load() -> ctypes.CDLL:
 class LaunchInfo(ctypes.Structure):
     """kfmi_launch_info of include/kfmi.h."""
     _fields_ = [("kernel", ctypes.c_char * 96), ("grid", ctypes.c_int64), ("block", ctypes.c_int32),
-                ("registers", ctypes.c_int32), ("lds_bytes", ctypes.c_int32), ("scratch_bytes", ctypes.c_int32)]
+                ("registers", ctypes.c_int32), ("lds_bytes", ctypes.c_int32), ("scratch_bytes", ctypes.c_int32),
+                ("plan", ctypes.c_char * 64)]
+
+
+def attention_kernel(b: int, hq: int, hkv: int, s: int, d: int, causal: bool, mode: int) -> str:
+    """Name (a key of KERNELS) of the attention kernel that a call of this
+    shape and mode launches on the current device under the calling
+    thread's overrides (kfmi_attention_kernel)."""
+    lib = load()
+    k = lib.kfmi_attention_kernel(b, hq, hkv, s, d, int(bool(causal)), mode)
+    if k < 0:
+        raise ValueError(f"kfmi_attention_kernel: {lib.kfmi_last_error().decode(errors='replace')}")
+    return {v: n for n, v in KERNELS.items()}[k]
 
 
 class Tuning(ctypes.Structure):
@@ -150,12 +164,14 @@ class tuning:
 def last_launches(max_records: int = 8) -> list[dict]:
     """The kernels launched by this thread's last successful compute call
     (kfmi_last_launches), in launch order: kernel instance, workgroups,
-    threads per workgroup, registers per thread, static LDS and scratch bytes."""
+    threads per workgroup, registers per thread, static LDS and scratch bytes,
+    and the launch-time choices (``plan``, e.g. "hpg=2 persistent=1 xcd=1")."""
     lib = load()
     buf = (LaunchInfo * max_records)()
     n = lib.kfmi_last_launches(buf, max_records)
     return [{"kernel": r.kernel.decode(errors="replace"), "grid": r.grid, "block": r.block,
-             "registers": r.registers, "lds_bytes": r.lds_bytes, "scratch_bytes": r.scratch_bytes}
+             "registers": r.registers, "lds_bytes": r.lds_bytes, "scratch_bytes": r.scratch_bytes,
+             "plan": r.plan.decode(errors="replace")}
             for r in buf[:min(n, max_records)]]
 
 

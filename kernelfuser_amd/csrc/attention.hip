@@ -365,51 +365,6 @@ hipError_t dispatch_pro(const AttnParams &p, int pro, int st, int kind, int bloc
   return hipErrorInvalidValue;
 }
 
-}  // namespace
-
-// Kernel choice by shape.  The ping-pong kernel needs D = 128 and an even GQA
-// ratio and pays off from 24 query blocks of 128 rows (S > 2944): below that,
-// its per-item Q prologues and 2-4 tile rounds per CU leave the chip
-// unbalanced and the general kernel (two 4-wave workgroups per CU) is faster
-// (measured on MI355X: S=2048 causal 50.8 vs 56.9 us with the ping-pong
-// kernel, B=4 S=1000 53.1 vs 56.8 us; S=4096 145 vs 134 us).  The wide
-// kernel runs only when the tuning overrides ask for it: one wave per SIMD
-// issues the softmax's VALU work and the MFMA stream by itself, and measures
-// 5-8% slower than the ping-pong kernel at S=4096 and 8192.
-int attention_kernel_by_shape(int64_t Hq, int64_t Hkv, int64_t S, int64_t D) {
-  constexpr int64_t PP_MIN_QBLOCKS = 24;
-  const int64_t G = Hq / Hkv;
-  if (D != 128 || (S + 127) / 128 < PP_MIN_QBLOCKS) return KFMI_KERNEL_GENERAL;
-  if (G % 2 == 0) return KFMI_KERNEL_PINGPONG;
-  return KFMI_KERNEL_GENERAL;
-}
-
-const char *attention_tuning_error(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full) {
-  (void)S;
-  const kfmi_tuning &t = thread_tuning();
-  const int64_t G = Hq / Hkv;
-  const int k = full ? KFMI_KERNEL_GENERAL : t.attn_kernel;
-  if (k == KFMI_KERNEL_PINGPONG && (D != 128 || G % 2 != 0))
-    return "the ping-pong kernel needs D == 128 and an even Hq/Hkv";
-  if (k == KFMI_KERNEL_WIDE && (D != 128 || G % 4 != 0))
-    return "the wide kernel needs D == 128 and Hq/Hkv divisible by 4";
-  if (t.pp_heads == 2 && G % 4 != 0 && attention_kernel(Hq, Hkv, S, D, full) == KFMI_KERNEL_PINGPONG)
-    return "four heads per ping-pong item need Hq/Hkv divisible by 4";
-  return nullptr;
-}
-
-int attention_kernel(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full) {
-  if (full) return KFMI_KERNEL_GENERAL;
-  const int k = thread_tuning().attn_kernel;
-  return k != KFMI_KERNEL_AUTO ? k : attention_kernel_by_shape(Hq, Hkv, S, D);
-}
-
-}  // namespace kfmi
-
-namespace kfmi {
-
-namespace {
-
 // Compute units of the current device (256 on MI355X), cached per device;
 // 256 when no device can be queried.  Scheduling only: results never depend
 // on it.
@@ -426,18 +381,106 @@ int64_t device_cus() {
   return v;
 }
 
+struct PpGrid {
+  int hpg;
+  int64_t n_qblocks, npairs, items, units;
+  bool xcd_remap, persistent;
+};
+
+// Geometry of the ping-pong kernel's grid: items of hpg Q heads per wave
+// group (two heads x 128 rows for hpg 1, four heads x 64 rows for hpg 2),
+// and whether the persistent long/short pairing applies (causal, the pairs
+// of every (long, short) item fill all CUs equally, XCD-remapped heads).
+PpGrid pp_grid(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, bool causal, int hpg, int64_t cus) {
+  PpGrid g;
+  const int64_t G = Hq / Hkv;
+  g.hpg = hpg;
+  g.n_qblocks = (S + 128 / hpg - 1) / (128 / hpg);
+  g.npairs = B * Hkv * (G / (2 * hpg));
+  g.xcd_remap = (B * Hkv) % 8 == 0 && g.npairs % 8 == 0;
+  g.items = g.n_qblocks * g.npairs;
+  g.units = g.npairs * ((g.n_qblocks + 1) / 2);
+  g.persistent = causal && g.xcd_remap && cus % 8 == 0 && g.units % cus == 0;
+  return g;
+}
+
+int pp_heads_for(int64_t Hq, int64_t Hkv) {
+  const int t = thread_tuning().pp_heads;
+  return t ? t : (Hq / Hkv) % 4 == 0 ? 2 : 1;
+}
+
+}  // namespace
+
+// Kernel choice by shape, from the tuning runner's measurements on MI355X
+// (every alternative gated and timed per shape).  The ping-pong kernel needs
+// D = 128 and an even GQA ratio and runs one 512-thread workgroup per CU;
+// below 16 query blocks of 128 rows its per-item Q prologues and few items
+// per CU lose to the general kernel (two 4-wave workgroups per CU): B=1
+// S=1024 27 vs 33 us, B=4 S=1000 causal a tie at 58 us.  From 16 blocks on
+// it wins when its items fill whole rounds of CUs: non-causal, when the item
+// count is a multiple of the CU count (S=2048 74.8 vs 78.4 us; S=3072, 1.5
+// rounds, 169 vs 156 us for the general kernel); causal, when the persistent
+// pairing applies (Qwen3-32B S=2048 78 vs 83 us; Qwen3-8B S=2048, half the
+// CUs paired, 61.5 vs 54.2 us) and always from 24 blocks (S=3072 93.7 vs
+// 97.2 us, S=4096 141 vs 153 us).  The wide kernel runs only when the
+// tuning overrides ask for it: one wave per SIMD issues the softmax's VALU
+// work and the MFMA stream by itself, and it measures 5-12% slower than the
+// ping-pong kernel from S=3072 on.
+int attention_kernel_by_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal) {
+  const int64_t G = Hq / Hkv;
+  const int64_t qb128 = (S + 127) / 128;
+  if (D != 128 || G % 2 != 0 || qb128 < 16) return KFMI_KERNEL_GENERAL;
+  if (causal && qb128 >= 24) return KFMI_KERNEL_PINGPONG;
+  const int64_t cus = device_cus();
+  const PpGrid g = pp_grid(B, Hq, Hkv, S, causal, pp_heads_for(Hq, Hkv), cus);
+  const bool fills = causal ? g.persistent && thread_tuning().persistent != 1 : g.items % cus == 0;
+  return fills ? KFMI_KERNEL_PINGPONG : KFMI_KERNEL_GENERAL;
+}
+
+const char *attention_tuning_error(int64_t Hq, int64_t Hkv, int64_t D, bool full) {
+  const kfmi_tuning &t = thread_tuning();
+  const int64_t G = Hq / Hkv;
+  const int k = full ? KFMI_KERNEL_GENERAL : t.attn_kernel;
+  if (k == KFMI_KERNEL_PINGPONG && (D != 128 || G % 2 != 0))
+    return "the ping-pong kernel needs D == 128 and an even Hq/Hkv";
+  if (k == KFMI_KERNEL_WIDE && (D != 128 || G % 4 != 0))
+    return "the wide kernel needs D == 128 and Hq/Hkv divisible by 4";
+  // wherever the ping-pong kernel may run (forced, or chosen by shape)
+  const bool pp_possible = k == KFMI_KERNEL_PINGPONG || (k == KFMI_KERNEL_AUTO && D == 128 && G % 2 == 0);
+  if (t.pp_heads == 2 && G % 4 != 0 && pp_possible)
+    return "four heads per ping-pong item need Hq/Hkv divisible by 4";
+  return nullptr;
+}
+
+int attention_kernel(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal, bool full) {
+  if (full) return KFMI_KERNEL_GENERAL;
+  const int k = thread_tuning().attn_kernel;
+  return k != KFMI_KERNEL_AUTO ? k : attention_kernel_by_shape(B, Hq, Hkv, S, D, causal);
+}
+
+}  // namespace kfmi
+
+namespace kfmi {
+
+namespace {
+
+
 // Split-KV plan for the general kernel at D = 256, which runs one workgroup
-// per CU: with no more work items than CUs, longest-first ordering cannot
+// per CU: with fewer work items than CUs, longest-first ordering cannot
 // balance a causal grid (the heaviest query block alone sets the time, and
 // no co-resident workgroup fills the gap).  Blocks with more key tiles than
 // half the maximum are then split into two halves of their key range (the
-// second holds the diagonal), and all items are listed longest first.  At
-// D = 128 two workgroups share each CU and one already keeps it nearly
-// busy, so the extra prologues of a split cost more than the balance gains.
+// second holds the diagonal), and all items are listed longest first.
+// Measured with the tuning runner: unsplit grids of 64-192 workgroups gain
+// 4-27% (Gemma-3-4B S=2048 57.2 vs 72.6 us), while a grid that already
+// fills every CU (Gemma-3-12B S=2048, 256 workgroups) loses 8% (83.1 vs
+// 77.0 us), so the plan needs fewer query blocks than CUs.  At D = 128 two
+// workgroups share each CU and one already keeps it nearly busy, so the
+// extra prologues of a split cost more than the balance gains.
 
 // Workspace layout: a counter region of the same size for every shape (one
 // 4-byte arrival counter per split (block, head) pair, at most
-// SPLIT_MAX_PAIRS; a plan has at most B*Hq*nqb <= CUs pairs), then the
+// SPLIT_MAX_PAIRS; a plan has fewer than B*Hq*nqb < CUs pairs), then the
 // partial results.  Because no shape's partials ever land in the counter
 // region and every launch leaves the counters it used at zero, a workspace
 // zero-filled once stays valid for any sequence of shapes launched on it.
@@ -452,7 +495,7 @@ struct SplitPlan {
 bool plan_split(int64_t B, int64_t Hq, int64_t S, int64_t D, bool causal, int64_t cus, SplitPlan &pl) {
   const int64_t BM = 128, BN = D == 128 ? 64 : 32;
   const int64_t nqb = (S + BM - 1) / BM;
-  if (D != 256 || !causal || nqb < 2 || B * Hq * nqb > cus) return false;
+  if (D != 256 || !causal || nqb < 2 || B * Hq * nqb >= cus) return false;
   auto tiles = [&](int64_t qb) { return ((qb + 1) * BM < S ? (qb + 1) * BM : S) + BN - 1; };
   const int64_t t_max = tiles(nqb - 1) / BN;
   const int64_t half = (t_max + 1) / 2;
@@ -525,25 +568,24 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   p.c_scale = (float)((factored ? 1.0 / sqrt((double)a.D) : a.scale) * LOG2E);
   const int BM = 128;
   p.n_qblocks = (int)((a.S + BM - 1) / BM);
-  const int G = p.Hq / p.Hkv;
   const kfmi_tuning &tun = thread_tuning();
-  const int kind = attention_kernel(a.Hq, a.Hkv, a.S, a.D, a.gk != nullptr);
+  const int kind = attention_kernel(a.B, a.Hq, a.Hkv, a.S, a.D, a.causal, a.gk != nullptr);
   if (kind == KFMI_KERNEL_PINGPONG && a.vt && a.S % 8 == 0) p.vt = a.vt;  // V^T rows must be 16-byte aligned
-  int blocks;
+  int blocks, n_split = 0;
   if (kind == KFMI_KERNEL_PINGPONG || kind == KFMI_KERNEL_WIDE) {
     // items of hpg Q heads per wave group: the wide kernel's four heads x 64
     // rows, or the ping-pong kernel's two heads x 128 rows (hpg 1) or four x
     // 64 (hpg 2)
-    p.pp_hpg = kind == KFMI_KERNEL_WIDE ? 2 : tun.pp_heads ? tun.pp_heads : G % 4 == 0 ? 2 : 1;
-    p.n_qblocks = (int)((a.S + BM / p.pp_hpg - 1) / (BM / p.pp_hpg));
-    const int npairs = p.B * p.Hkv * (G / (2 * p.pp_hpg));
-    p.xcd_remap = ((p.B * p.Hkv) % 8 == 0 && npairs % 8 == 0) ? 1 : 0;
-    blocks = p.n_qblocks * npairs;
-    // persistent mode when the (long, short) pairs fill every CU equally
     const int64_t cus = device_cus();
-    const int64_t units = (int64_t)npairs * ((p.n_qblocks + 1) / 2);
-    if (a.causal && p.xcd_remap && cus % 8 == 0 && units % cus == 0 && tun.persistent != 1) {
-      p.pp_units = (int)units;
+    const PpGrid g = pp_grid(a.B, a.Hq, a.Hkv, a.S, a.causal, kind == KFMI_KERNEL_WIDE ? 2 : pp_heads_for(a.Hq, a.Hkv),
+                             cus);
+    p.pp_hpg = g.hpg;
+    p.n_qblocks = (int)g.n_qblocks;
+    p.xcd_remap = g.xcd_remap ? 1 : 0;
+    blocks = (int)g.items;
+    // persistent mode when the (long, short) pairs fill every CU equally
+    if (g.persistent && tun.persistent != 1) {
+      p.pp_units = (int)g.units;
       blocks = (int)cus;
     }
   } else {
@@ -554,6 +596,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     if (a.work && tun.split != 1 && plan_split(a.B, a.Hq, a.S, a.D, a.causal, device_cus(), pl)) {
       const int64_t pairs = (int64_t)pl.n_split * nbh;
       if (a.work_bytes >= SPLIT_COUNTER_BYTES + split_partial_bytes(pairs, a.D)) {
+        n_split = pl.n_split;
         p.n_items = pl.n_items;
         for (int i = 0; i < pl.n_items; ++i) {
           p.it_qb[i] = pl.qb[i]; p.it_t0[i] = pl.t0[i]; p.it_t1[i] = pl.t1[i]; p.it_sid[i] = pl.sid[i];
@@ -570,12 +613,19 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     if (a.causal && a.D == 128 && p.n_items == 0 && cus % nbh == 0 && blocks > cus && blocks <= 2 * cus)
       p.slot2 = (int)cus;
   }
+  hipError_t e;
   if (a.D == 128) {
-    return a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, kind, blocks, stream)
-                    : dispatch_pro<128, 64, false>(p, a.prologue, a.style, kind, blocks, stream);
+    e = a.causal ? dispatch_pro<128, 64, true>(p, a.prologue, a.style, kind, blocks, stream)
+                 : dispatch_pro<128, 64, false>(p, a.prologue, a.style, kind, blocks, stream);
+  } else {
+    e = a.causal ? dispatch_pro<256, 32, true>(p, a.prologue, a.style, KFMI_KERNEL_GENERAL, blocks, stream)
+                 : dispatch_pro<256, 32, false>(p, a.prologue, a.style, KFMI_KERNEL_GENERAL, blocks, stream);
   }
-  return a.causal ? dispatch_pro<256, 32, true>(p, a.prologue, a.style, KFMI_KERNEL_GENERAL, blocks, stream)
-                  : dispatch_pro<256, 32, false>(p, a.prologue, a.style, KFMI_KERNEL_GENERAL, blocks, stream);
+  if (kind == KFMI_KERNEL_PINGPONG || kind == KFMI_KERNEL_WIDE)
+    launch_log_plan("hpg=%d persistent=%d xcd=%d", p.pp_hpg, p.pp_units > 0 ? 1 : 0, p.xcd_remap);
+  else
+    launch_log_plan("split=%d pair=%d xcd=%d", n_split, p.slot2 > 0 ? 1 : 0, p.xcd_remap);
+  return e;
 }
 
 }  // namespace kfmi

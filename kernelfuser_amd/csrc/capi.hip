@@ -73,6 +73,14 @@ void launch_log_add(const void *fn, const char *name, int64_t grid, int block) {
   g_launches.push_back(r);
 }
 
+void launch_log_plan(const char *fmt, ...) {
+  if (g_launches.empty()) return;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_launches.back().plan, sizeof(g_launches.back().plan), fmt, ap);
+  va_end(ap);
+}
+
 }  // namespace kfmi
 
 namespace {
@@ -204,8 +212,8 @@ int kfmi_prepare_bf16(const void *q, const void *k, const void *v, const void *g
 }
 
 // The thread's dispatch overrides must be able to run this shape.
-static int check_tuning(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full) {
-  const char *why = kfmi::attention_tuning_error(Hq, Hkv, S, D, full);
+static int check_tuning(int64_t Hq, int64_t Hkv, int64_t D, bool full) {
+  const char *why = kfmi::attention_tuning_error(Hq, Hkv, D, full);
   return why ? fail(KFMI_EINVAL, "kfmi_set_tuning: %s", why) : KFMI_OK;
 }
 
@@ -232,6 +240,17 @@ int64_t kfmi_attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64
   return kfmi::attention_workspace_bytes(B, Hq, Hkv, S, D, causal != 0);
 }
 
+int kfmi_attention_kernel(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, int causal, int mode) {
+  if (check_shape(B, Hq, Hkv, S, D) != KFMI_OK) return -KFMI_EINVAL;
+  if (mode != KFMI_MODE_QUERY && mode != KFMI_MODE_FULL && mode != KFMI_MODE_UNFUSED) {
+    fail(KFMI_EINVAL, "mode must be KFMI_MODE_QUERY, _FULL or _UNFUSED (got %d)", mode);
+    return -KFMI_EINVAL;
+  }
+  if (check_tuning(Hq, Hkv, D, mode == KFMI_MODE_FULL) != KFMI_OK) return -KFMI_EINVAL;
+  g_error.clear();
+  return kfmi::attention_kernel(B, Hq, Hkv, S, D, causal != 0, mode == KFMI_MODE_FULL);
+}
+
 static int check_work(const void *work, int64_t work_bytes) {
   if (work_bytes < 0) return fail(KFMI_EINVAL, "work_bytes must be >= 0");
   if (work && !aligned16(work)) return fail(KFMI_EINVAL, "work must be 16-byte aligned");
@@ -251,7 +270,7 @@ int kfmi_attention_bf16(const void *q, const void *k, const void *v, const void 
   if (fuse_q && cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
   KFMI_TRY(check_work(work, work_bytes));
-  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
+  KFMI_TRY(check_tuning(Hq, Hkv, D, false));
   KFMI_TRY(check_device());
   const int pro = !fuse_q ? kfmi::PRO_NONE : (cos ? kfmi::PRO_NORM_ROPE : kfmi::PRO_NORM);
   if (vt) KFMI_TRY(check_ptrs({{vt, "vt"}}));
@@ -283,19 +302,16 @@ static int launch_attention_entry(const void *q, const void *k, const void *v, c
   if ((cos == nullptr) != (sin == nullptr)) return fail(KFMI_EINVAL, "provide both rotary tables or neither");
   if (cos) KFMI_TRY(check_ptrs({{cos, "cos"}, {sin, "sin"}}));
   if (!(scale > 0.0)) return fail(KFMI_EINVAL, "scale must be > 0");
-  KFMI_TRY(check_tuning(Hq, Hkv, S, D, mode == KFMI_MODE_FULL));
+  KFMI_TRY(check_tuning(Hq, Hkv, D, mode == KFMI_MODE_FULL));
   KFMI_TRY(check_device());
   int64_t clear_bytes = 0;
   if (noalloc) {
+    // A plan larger than the static array runs unsplit (no workspace), as
+    // kfmi_launch_attention_bf16 does when given none.
     const int64_t need = kfmi::attention_workspace_bytes(B, Hq, Hkv, S, D, causal != 0);
-    if (need > KFMI_SCRATCH_BYTES)
-      return fail(KFMI_EINVAL,
-                  "split-KV workspace of %lld bytes exceeds the static scratch of %lld bytes "
-                  "(use kfmi_launch_attention_bf16 with a caller workspace for this shape)",
-                  (long long)need, (long long)KFMI_SCRATCH_BYTES);
     work = nullptr;
     work_bytes = 0;
-    if (need > 0) {
+    if (need > 0 && need <= KFMI_SCRATCH_BYTES) {
       hipError_t e = kfmi::noalloc_scratch(&work);
       if (e != hipSuccess) return launch_status(e, "static scratch address");
       work_bytes = KFMI_SCRATCH_BYTES;
@@ -314,7 +330,7 @@ static int launch_attention_entry(const void *q, const void *k, const void *v, c
   }
   const bool rope = cos != nullptr;
   // V^T is used by the ping-pong kernel when its rows are 16-byte aligned.
-  const bool use_vt = vt != nullptr && kfmi::attention_kernel(Hq, Hkv, S, D, false) == KFMI_KERNEL_PINGPONG && S % 8 == 0;
+  const bool use_vt = vt != nullptr && kfmi::attention_kernel(B, Hq, Hkv, S, D, causal != 0, false) == KFMI_KERNEL_PINGPONG && S % 8 == 0;
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;
   r.cos = (const uint16_t *)cos; r.sin = (const uint16_t *)sin; r.qn = (uint16_t *)qn; r.kn = (uint16_t *)kn;
@@ -384,7 +400,7 @@ int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, f
   if (inv_mode != 0 && inv_mode != 1) return fail(KFMI_EINVAL, "inv_mode must be 0 (read) or 1 (compute)");
   if (inv_mode == 0) KFMI_TRY(check_ptrs({{inv, "inv"}}));
   if (inv && (reinterpret_cast<uintptr_t>(inv) & 3u)) return fail(KFMI_EINVAL, "inv must be 4-byte aligned");
-  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
+  KFMI_TRY(check_tuning(Hq, Hkv, D, false));
   KFMI_TRY(check_device());
   const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
   return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
@@ -398,7 +414,7 @@ int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void
   KFMI_TRY(check_tiles(bm, bn));
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}, {inv, "inv"}, {kn, "kn"}}));
   if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
-  KFMI_TRY(check_tuning(Hq, Hkv, S, D, false));
+  KFMI_TRY(check_tuning(Hq, Hkv, D, false));
   KFMI_TRY(check_device());
   kfmi::RowsArgs r{};
   r.q = (const uint16_t *)q; r.k = (const uint16_t *)k; r.gq = (const uint16_t *)gq; r.gk = (const uint16_t *)gk;

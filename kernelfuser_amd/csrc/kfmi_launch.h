@@ -59,6 +59,8 @@ struct AttnArgs {
 // instance, its grid and block and the runtime's resource figures for it.
 void launch_log_clear();
 void launch_log_add(const void *fn, const char *name, int64_t grid, int block);
+// printf-style plan string of the last logged launch (kfmi_launch_info.plan)
+void launch_log_plan(const char *fmt, ...);
 inline const char *tf(bool b) { return b ? "true" : "false"; }
 
 hipError_t launch_rows(const RowsArgs &a, hipStream_t stream);
@@ -70,9 +72,9 @@ const kfmi_tuning &thread_tuning();
 // The attention kernel (KFMI_KERNEL_GENERAL / _PINGPONG / _WIDE) that
 // launch_attention runs for this shape under the thread's overrides; `full`
 // is mode 'full' (always the general kernel).
-int attention_kernel(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full);
-// Why the thread's overrides cannot run this shape (NULL: they can).
-const char *attention_tuning_error(int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool full);
+int attention_kernel(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal, bool full);
+// Why the thread's overrides cannot run this geometry (NULL: they can).
+const char *attention_tuning_error(int64_t Hq, int64_t Hkv, int64_t D, bool full);
 // Workspace bytes with which launch_attention splits the key range of the
 // longest causal query blocks over two workgroups (0: this shape never splits).
 int64_t attention_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int64_t D, bool causal);

@@ -123,13 +123,19 @@ __device__ __forceinline__ float row_sum(float x) {
 #ifndef KFMI_ROWS_NT
 #define KFMI_ROWS_NT 1
 #endif
-// Heads per workgroup (rows per lane) of rows_kernel: two, or four for
-// Q+K launches of at least 2^18 rows with S <= 4096 at D = 128 (1.2-1.5
-// points of HBM peak more at B >= 4, S <= 2048; 0.8 less at B = 1, S = 8192;
-// fewer, longer workgroups lose on small launches, and the K-only
-// preparation is faster with two).
+// Heads per workgroup (rows per lane) of rows_kernel: two, or four for Q+K
+// launches at D = 128 where the tuning runner measured four faster:
+// - FP32 style, at least 2^18 rows with S <= 4096: 27.2 vs 28.1-28.4 us at
+//   the 170 MB shapes (B >= 4), a tie at B = 1, S = 2048 and S = 8192;
+// - HF and legacy styles, whose per-row arithmetic is longer, from 2^15 to
+//   2^17 rows: 8.2 vs 9.9 us at B = 1, S = 2048 (16-21% from 40k to 82k rows,
+//   3-5% at 123k-164k), while two heads are 1-3% faster at 160k rows and
+//   more.
+// Fewer, longer workgroups lose on small launches (below 2^15 rows), and
+// the K-only preparation is faster with two.
 constexpr int ROWS_HPW = 2, ROWS_HPW_BIG = 4;
 constexpr int64_t ROWS_BIG = (int64_t)1 << 18, ROWS_BIG_MAX_S = 4096;
+constexpr int64_t ROWS_MID_MIN = (int64_t)1 << 15, ROWS_MID_END = (int64_t)1 << 17;
 __device__ __forceinline__ u32x4_t ld_row(const uint16_t *p) { return KFMI_ROWS_NT ? ld16_nt(p) : ld16(p); }
 __device__ __forceinline__ void st_row(uint16_t *p, const u32x4_t &v) {
   if (KFMI_ROWS_NT) st16_nt(p, v); else st16(p, v);
@@ -346,15 +352,18 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   const int64_t rows = (int64_t)(p.heads_q + p.heads_k) * a.S;
   const bool big_ok = a.D == 128 && !a.only_k && !a.vt && a.style != ST_FACTORED;  // where the 4-head form exists
   const int forced = thread_tuning().rows_heads;
-  p.hpw = big_ok && (forced ? forced == ROWS_HPW_BIG : rows >= ROWS_BIG && a.S <= ROWS_BIG_MAX_S) ? ROWS_HPW_BIG
-                                                                                                   : ROWS_HPW;
+  const bool big_by_shape = a.style == ST_FP32 ? rows >= ROWS_BIG && a.S <= ROWS_BIG_MAX_S
+                                               : rows >= ROWS_MID_MIN && rows < ROWS_MID_END;
+  p.hpw = big_ok && (forced ? forced == ROWS_HPW_BIG : big_by_shape) ? ROWS_HPW_BIG : ROWS_HPW;
   const int64_t units = (p.heads_q + p.hpw - 1) / p.hpw + (p.heads_k + p.hpw - 1) / p.hpw;
   p.row_blocks = (uint32_t)(units * p.nblk);
   p.vt_sblocks = (int)((a.S + 63) / 64);
   p.vt_tiles = a.vt ? a.B * a.Hkv * p.vt_sblocks : 0;
   if (a.vt && a.D != 128) return hipErrorInvalidValue;
-  if (a.D == 128) return dispatch_rows<128>(p, a.style, a.rope, a.only_k, stream);
-  return dispatch_rows<256>(p, a.style, a.rope, a.only_k, stream);
+  const hipError_t e = a.D == 128 ? dispatch_rows<128>(p, a.style, a.rope, a.only_k, stream)
+                                   : dispatch_rows<256>(p, a.style, a.rope, a.only_k, stream);
+  launch_log_plan("hpw=%d", (int)p.hpw);
+  return e;
 }
 
 }  // namespace kfmi

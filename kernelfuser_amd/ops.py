@@ -74,11 +74,15 @@ def _style(norm_style: Optional[str], hf_norm: bool) -> int:
 # larger shape needs more, a new buffer
 # replaces it in the cache; the old one stays referenced until the process
 # ends, so nothing that ever held its address sees it freed.  A launch
-# captured into a HIP graph never uses the cache: it gets its own zero-filled
-# buffer from the graph's private memory pool (the fill is part of the graph
-# and runs before the launch on every replay), so replays, on whatever
-# stream, never share a workspace with eager launches or with other graphs.
+# captured into a HIP graph never uses the cache: it gets its own buffer from
+# the graph's private memory pool whose counter region (the first
+# WORK_COUNTER_BYTES; the partials behind it are written before they are
+# read) is zeroed by a fill that is part of the graph and runs before the
+# launch on every replay, so replays, on whatever stream, never share a
+# workspace with eager launches or with other graphs.
 # ---------------------------------------------------------------------------
+
+WORK_COUNTER_BYTES = 4096  # the workspace's arrival-counter region (include/kfmi.h)
 
 _work_cache: dict[tuple[int, int], torch.Tensor] = {}
 _work_retired: list[torch.Tensor] = []
@@ -100,13 +104,15 @@ def attention_workspace_bytes(b: int, hq: int, hkv: int, s: int, d: int, causal:
 
 
 def _workspace(device: torch.device, nbytes: int):
-    """A zero-filled workspace of at least nbytes on this device: the current
-    stream's cached one for eager launches, a new one from the graph's pool
-    during capture; None when nbytes is 0."""
+    """A workspace of at least nbytes on this device with zeroed counters:
+    the current stream's cached one (zero-filled once) for eager launches, a
+    new one from the graph's pool during capture; None when nbytes is 0."""
     if nbytes <= 0:
         return None
     if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        buf[:WORK_COUNTER_BYTES].zero_()  # a fill kernel inside the graph, not a memset node
+        return buf
     idx = device.index if device.index is not None else torch.cuda.current_device()
     stream = torch.cuda.current_stream(torch.device("cuda", idx))
     key = (idx, stream.cuda_stream)
@@ -461,14 +467,12 @@ def _optimized_attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g
     return out
 
 
-PP_MIN_QBLOCKS = 24  # the library runs its ping-pong kernel from 24 query blocks of 128 rows
-
-
-def uses_vt(hq: int, hkv: int, s: int, d: int) -> bool:
-    """Whether launch_attention makes use of a ``vt`` scratch for this shape
-    (the library's ping-pong kernel: D=128, even GQA ratio, S > 2944, and
-    16-byte aligned V^T rows)."""
-    return d == 128 and (hq // hkv) % 2 == 0 and -(-s // 128) >= PP_MIN_QBLOCKS and s % 8 == 0
+def uses_vt(hq: int, hkv: int, s: int, d: int, b: int = 1, causal: bool = True) -> bool:
+    """Whether launch_attention (mode 'query' or 'unfused') makes use of a
+    ``vt`` scratch for this shape on the current device: when the library
+    runs its ping-pong kernel for it (``kfmi_attention_kernel``) and V^T rows
+    are 16-byte aligned (S % 8 == 0)."""
+    return s % 8 == 0 and _lib.attention_kernel(b, hq, hkv, s, d, causal, MODE_QUERY) == "pingpong"
 
 
 @_optimized_attention_op.register_fake

@@ -41,7 +41,8 @@ reference's Qwen3-8B RoPE grid (S 128-512, B 1/8/32, causal and not);
 ``--grid norope`` the historical no-RoPE rows of every model (B=1, S 128-2048),
 ``--grid factored`` their Gemma-3 rows, ``--grid configs`` this build's
 measured configurations (Qwen3-8B B=1 S=2048/4096/8192, B=4 S=1000; Gemma-3-12B
-factored B=2 S=2048).
+factored B=2 S=2048), and ``--grid tune`` the tuning runner of module
+``tune`` (the counterpart of ``tune_refinement``, rope:765-814).
 """
 from __future__ import annotations
 
@@ -310,7 +311,7 @@ def tail_checks(device="cuda:0"):
 
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
-    ap.add_argument("--grid", default="rope", choices=["rope", "norope", "factored", "configs"])
+    ap.add_argument("--grid", default="rope", choices=["rope", "norope", "factored", "configs", "tune"])
     ap.add_argument("--out", required=True)
     ap.add_argument("--models", default="")
     ap.add_argument("--sequences", default="")
@@ -319,7 +320,10 @@ def main(argv=None):
     ap.add_argument("--launches", type=int, default=20)
     ap.add_argument("--no-tails", action="store_true")
     args = ap.parse_args(argv)
-    rows = grid(args.grid)
+    rows = grid(args.grid) if args.grid != "tune" else None
+    if rows is None:
+        from . import tune
+        rows = tune.SHAPES
     if args.models:
         rows = [r for r in rows if r[0] in args.models.split(",")]
     if args.sequences:
@@ -330,6 +334,11 @@ def main(argv=None):
         rows = [r for r in rows if r[3] == (args.causal == "true")]
     if not rows:
         ap.error("no refinement rows selected")
+    if args.grid == "tune":
+        out = Path(args.out)
+        out.parent.mkdir(parents=True, exist_ok=True)
+        return tune.run(rows, launches=args.launches,
+                        save=lambda rec: out.write_text(json.dumps(rec, indent=1) + "\n"))
     rec = {"schema": "kernelfuser-amd-refine-v1", "grid": args.grid,
            "created_utc": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime()),
            "environment": {"gpu": torch.cuda.get_device_name(0), "torch": torch.__version__,

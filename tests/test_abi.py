@@ -27,7 +27,7 @@ def lib():
 def test_header_declares_the_bound_entry_points():
     names = _declared()
     queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes", "kfmi_last_launches",
-               "kfmi_set_tuning", "kfmi_get_tuning"}
+               "kfmi_set_tuning", "kfmi_get_tuning", "kfmi_attention_kernel"}
     assert queries <= set(names)
     assert set(_lib.SIGNATURES) == set(names) - queries
 
@@ -114,14 +114,39 @@ def test_workspace_bytes_query(lib):
     assert f(1, 32, 8, 2048, 128, 1) == 0  # D = 128: two workgroups per CU, no split
     assert f(1, 16, 8, 2048, 256, 0) == 0  # not causal: nothing to balance
     assert f(4, 16, 8, 2048, 256, 1) == 0  # more work items than CUs
-    n = f(1, 16, 8, 2048, 256, 1)  # 256 items = 256 CUs: the long blocks split
-    # 8 split blocks x 16 heads: a 4 KiB counter region (the same for every
+    assert f(1, 16, 8, 2048, 256, 1) == 0  # 256 items = 256 CUs: already one per CU
+    n = f(1, 8, 4, 2048, 256, 1)  # 128 items on 256 CUs: the long blocks split
+    # 8 split blocks x 8 heads: a 4 KiB counter region (the same for every
     # shape) + 2 halves of 256 threads x (128 + 2) floats per pair
-    pairs = 8 * 16
+    pairs = 8 * 8
     assert n == 4096 + pairs * 2 * 130 * 256 * 4
     # a 12-pair plan keeps the same counter region: its partials start where
-    # the 128-pair plan's do
+    # the 64-pair plan's do
     assert f(1, 4, 2, 640, 256, 1) == 4096 + 12 * 2 * 130 * 256 * 4
+
+
+def test_attention_kernel_query(lib):
+    """The kernel choice by shape, as measured by the tuning runner (CU
+    count 256 where no device can be queried)."""
+    k = lambda *a: _lib.attention_kernel(*a)
+    assert k(1, 32, 8, 2048, 128, True, 0) == "general"     # causal, 16 blocks: half the CUs paired
+    assert k(1, 32, 8, 3072, 128, True, 0) == "pingpong"    # causal, 24 blocks
+    assert k(1, 64, 8, 2048, 128, True, 0) == "pingpong"    # Qwen3-32B: the pairing fills every CU
+    assert k(1, 32, 8, 2048, 128, False, 0) == "pingpong"   # 256 items: one round
+    assert k(1, 32, 8, 3072, 128, False, 0) == "general"    # 384 items: 1.5 rounds
+    assert k(4, 32, 8, 1000, 128, True, 0) == "general"     # 8 blocks
+    assert k(1, 32, 8, 8192, 128, True, 2) == "general"     # mode 'full'
+    assert k(1, 16, 8, 8192, 256, True, 0) == "general"     # D = 256
+    assert k(1, 40, 8, 8192, 128, True, 0) == "general"     # odd GQA ratio
+    with _lib.tuning(attn_kernel="wide"):
+        assert k(4, 32, 8, 1000, 128, True, 0) == "wide"
+    with _lib.tuning(persistent=1):
+        assert k(1, 64, 8, 2048, 128, True, 0) == "general"  # without the pairing the grid does not fill
+    assert lib.kfmi_attention_kernel(1, 32, 8, 0, 128, 1, 0) == -EINVAL
+    assert lib.kfmi_attention_kernel(1, 32, 8, 16, 128, 1, 7) == -EINVAL
+    with _lib.tuning(attn_kernel="pingpong"):
+        assert lib.kfmi_attention_kernel(1, 16, 8, 16, 256, 1, 0) == -EINVAL
+        assert "ping-pong" in _err(lib)
 
 
 def test_call_maps_einval_to_value_error(lib):

@@ -243,7 +243,7 @@ def test_vt_path_identical(gpu, b, s, causal):
     assert bool((diff <= tol).all()), float((diff / tol).max())
     assert float((diff > 0).float().mean()) < 0.02
     assert torch.equal(kn1, kn2)
-    if uses_vt(32, 8, s, 128):
+    if uses_vt(32, 8, s, 128, b, causal):
         assert torch.equal(vt, xs.v.transpose(2, 3).contiguous().view_as(vt))
     else:
         assert bool((vt == 3.0).all())

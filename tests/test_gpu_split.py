@@ -1,7 +1,7 @@
 """Split-KV execution of the general attention kernel at D = 256 (one
-workgroup per CU): for causal shapes whose work items would just fill the
-GPU, the longest query blocks' key ranges are split over two workgroups and
-merged by the one finishing second.
+workgroup per CU): for causal shapes with fewer work items than CUs, the
+longest query blocks' key ranges are split over two workgroups and merged by
+the one finishing second.
 
 Results are bit-identical from launch to launch (the merge runs in a fixed
 order whichever half performs it), within a few ulp of the unsplit launch
@@ -25,7 +25,7 @@ def _run(xs, kn, causal, work, style="fp32"):
     return out
 
 
-@pytest.mark.parametrize("geom,b,s", [((16, 8, 256), 1, 2048), ((16, 8, 256), 1, 1900), ((8, 4, 256), 1, 2048),
+@pytest.mark.parametrize("geom,b,s", [((16, 8, 256), 1, 1536), ((16, 8, 256), 1, 1900), ((8, 4, 256), 1, 2048),
                                       ((4, 2, 256), 1, 1000)])
 def test_split_matches_unsplit(gpu, geom, b, s):
     hq, hkv, d = geom
@@ -57,10 +57,10 @@ def test_split_matches_unsplit(gpu, geom, b, s):
 
 
 def test_split_graph_replays(gpu):
-    xs = make_inputs(1, 2048, (16, 8, 256), 1313).to(gpu)
+    xs = make_inputs(1, 1536, (16, 8, 256), 1313).to(gpu)
     kn = torch.empty_like(xs.k)
     prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="hf")
-    work = torch.zeros(attention_workspace_bytes(1, 16, 8, 2048, 256, True), dtype=torch.uint8, device=gpu)
+    work = torch.zeros(attention_workspace_bytes(1, 16, 8, 1536, 256, True), dtype=torch.uint8, device=gpu)
     out = torch.empty_like(xs.q)
     fn = lambda: attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin, causal=True,
                                    norm_style="hf", work=work)
@@ -92,7 +92,7 @@ def test_split_cached_workspace_per_stream(gpu):
     """With work=None each (device, stream) gets its own cached workspace, so
     split launches on two streams at once do not share counters or partials:
     both streams reproduce the single-stream result bit for bit."""
-    xs = make_inputs(1, 2048, (16, 8, 256), 1515).to(gpu)
+    xs = make_inputs(1, 1536, (16, 8, 256), 1515).to(gpu)
     kn = torch.empty_like(xs.k)
     prepare_attention(xs.reference7, None, kn, only_k=True, norm_style="fp32")
     announce("split cached workspace on two streams")
@@ -118,20 +118,20 @@ def test_workspace_serves_any_shape_sequence(gpu):
     """One zero-filled workspace serves any sequence of split shapes: the
     arrival counters sit in a region of the same size for every shape and no
     shape's partial results land in it.  A 12-pair plan (Hq=4, S=640) run on
-    a workspace sized for a 128-pair plan (Hq=16, S=2048) leaves the larger
+    a workspace sized for a 96-pair plan (Hq=16, S=1536) leaves the larger
     plan's whole counter region at zero, and the larger shape then gives the
     same bits as on a fresh workspace."""
     small = make_inputs(1, 640, (4, 2, 256), 2121).to(gpu)
-    large = make_inputs(1, 2048, (16, 8, 256), 2222).to(gpu)
+    large = make_inputs(1, 1536, (16, 8, 256), 2222).to(gpu)
     kn_s, kn_l = torch.empty_like(small.k), torch.empty_like(large.k)
     prepare_attention(small.reference7, None, kn_s, only_k=True, norm_style="fp32")
     prepare_attention(large.reference7, None, kn_l, only_k=True, norm_style="fp32")
     nb_s = attention_workspace_bytes(1, 4, 2, 640, 256, True)
-    nb_l = attention_workspace_bytes(1, 16, 8, 2048, 256, True)
+    nb_l = attention_workspace_bytes(1, 16, 8, 1536, 256, True)
     per_pair = 2 * (256 // 2 + 2) * 256 * 4
-    assert 0 < nb_s < nb_l and nb_l // per_pair == 128 and nb_s // per_pair == 12
+    assert 0 < nb_s < nb_l and nb_l // per_pair == 96 and nb_s // per_pair == 12
     counter_region = nb_l - (nb_l // per_pair) * per_pair
-    announce("split workspace reused from a 12-pair to a 128-pair plan")
+    announce("split workspace reused from a 12-pair to a 96-pair plan")
     work = torch.zeros(nb_l, dtype=torch.uint8, device=gpu)
     for _ in range(2):
         _run(small, kn_s, True, work)
@@ -152,7 +152,7 @@ def test_captured_split_keeps_its_workspace(gpu):
     eager cache afterwards (a larger split shape on the same stream) must not
     disturb replays, which are compared bit for bit with eager results."""
     small = make_inputs(1, 2048, (8, 4, 256), 1717).to(gpu)
-    large = make_inputs(1, 2048, (16, 8, 256), 1818).to(gpu)
+    large = make_inputs(1, 1536, (16, 8, 256), 1818).to(gpu)
     kn_s, kn_l = torch.empty_like(small.k), torch.empty_like(large.k)
     prepare_attention(small.reference7, None, kn_s, only_k=True, norm_style="fp32")
     prepare_attention(large.reference7, None, kn_l, only_k=True, norm_style="fp32")
@@ -182,5 +182,5 @@ def test_captured_split_keeps_its_workspace(gpu):
         again = _run(small, kn_s, True, None)
         torch.cuda.synchronize()
         assert torch.equal(again, split), i
-    ref = oracle.oracle_rows_fp32(*[t.cpu() for t in large.astuple()], torch.arange(2040, 2048), True)
-    assert oracle.attention_gate(big[:, :, 2040:].cpu(), ref)["pass"]
+    ref = oracle.oracle_rows_fp32(*[t.cpu() for t in large.astuple()], torch.arange(1528, 1536), True)
+    assert oracle.attention_gate(big[:, :, 1528:].cpu(), ref)["pass"]

@@ -30,8 +30,8 @@ def _launch(xs_gpu, causal, mode="query", norm_style="fp32", rope=True, kernel="
     kn = torch.empty_like(xs_gpu.k)
     qn = torch.empty_like(q) if mode == "unfused" else None
     with _lib.tuning(attn_kernel=kernel, **tun):
-        recs = launch_attention((q, xs_gpu.k, xs_gpu.v, xs_gpu.gq, xs_gpu.gk, xs_gpu.cos, xs_gpu.sin), out,
-                                causal=causal, mode=mode, rope=rope, qn=qn, kn=kn, norm_style=norm_style)
+        recs = list(launch_attention((q, xs_gpu.k, xs_gpu.v, xs_gpu.gq, xs_gpu.gk, xs_gpu.cos, xs_gpu.sin), out,
+                                     causal=causal, mode=mode, rope=rope, qn=qn, kn=kn, norm_style=norm_style))
     torch.cuda.synchronize()
     return out.cpu(), recs
 
@@ -206,8 +206,8 @@ def test_lean_overflow_redo_huge_v(gpu, kernel):
 
 
 def test_pingpong_still_runs_s4096_rows(gpu):
-    """The ping-pong kernel, now behind the wide kernel at these shapes,
-    forced at S=4096 on a row sample."""
+    """The ping-pong kernel forced at S=4096 (its shape-based choice too)
+    beside the wide-kernel tests, on a row sample."""
     s = 4096
     xs = make_inputs(1, s, QWEN3_8B, 3909)
     announce("pingpong forced query fp32 B=1 S=4096 causal")
