@@ -9,7 +9,9 @@ B=1, S=4096, causal, theta=1e6 -- one step = both launches of
 ``launch_attention(mode='query')`` (K RMSNorm+RoPE once, then causal GQA flash
 attention with Q's RMSNorm+RoPE in the prologue), the reference's timing unit
 (rope:665-666).  ``value`` is causal TFLOP/s (4*B*Hq*D*S(S+1)/2 per step) over
-the K timed steps, inputs resident in HBM.
+the K timed steps, inputs resident in HBM; the K steps are recorded once into
+a HIP graph and replayed (the reference times graph replays too,
+fusion_harness.py:32-79), and the eager per-step figures ride along.
 
 The same line carries, as nested objects:
   * ``roofline``      -- the attention kernel alone, timed with HIP events on the
@@ -117,6 +119,7 @@ def headline(args, torch, kf):
         settle_steps += 20
         torch.cuda.synchronize()
     torch.cuda.synchronize()
+    # Eager steps: one host call per step.
     ev0, ev1 = _events()
     t0 = time.perf_counter()
     ev0.record()
@@ -124,12 +127,42 @@ def headline(args, torch, kf):
         step()
     ev1.record()
     torch.cuda.synchronize()
+    eager_wall_ms = (time.perf_counter() - t0) * 1e3
+    eager_dev_ms = ev0.elapsed_time(ev1)
+    # The timed steps: the same K steps recorded once into a HIP graph and
+    # replayed, as the reference times its arms (fusion_harness.py:32-79);
+    # the replay is bracketed by synchronisations, so the host clock sees
+    # exactly the K steps' device work.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        step()
+        side.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(args.steps):
+                step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    t_settle = time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:  # the clock settles under the replayed load
+        graph.replay()
+        torch.cuda.synchronize()
+    ev0, ev1 = _events()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     dev_ms = ev0.elapsed_time(ev1)
+    del graph
     flops = kf.attention_flops(b, hq, s, d, True)
     ms_step = wall_ms / args.steps
     res = {"flops_per_step": flops, "ms_per_step": ms_step, "device_ms_per_step": dev_ms / args.steps,
-           "tflops": flops / (ms_step * 1e-3) / 1e12, "settle_steps": settle_steps}
+           "tflops": flops / (ms_step * 1e-3) / 1e12, "settle_steps": settle_steps,
+           "eager_ms_per_step": eager_wall_ms / args.steps, "eager_device_ms_per_step": eager_dev_ms / args.steps}
     # The two kernels separately (events on the launch stream).
     attn_ms = time_graph(lambda i: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
                                                            causal=True, fuse_q=True, norm_style=args.norm_style),
@@ -274,8 +307,9 @@ def pmc_run(torch, kf):
     for _ in range(3):
         kf.launch_factored_attention((fx.q, fx.k, fx.v, fx.gq, fx.gk), fo, finv, fk, causal=True, bm=128, bn=64)
     del fx, fo, fk, finv
-    # norm+RoPE: B=1 S=8192 runs two heads per workgroup, B=4 S=2048 four
-    for b, s in ((1, 8192), (4, 2048)):
+    # norm+RoPE: the six sweep shapes, in the sweep's order (the three B=1
+    # shapes run two heads per workgroup, the three 170 MB ones four)
+    for b, s in SWEEP:
         nr = kf.make_inputs(b, s, QWEN3_8B, 1909, with_v=False).to("cuda:0")
         qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)
         for _ in range(3):
@@ -287,7 +321,7 @@ def pmc_run(torch, kf):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_run": True, "copy_bytes_each_way": src.numel() * 4,
-                      "attention": "B=1 S=4096 causal", "general": ["B=1 S=2048", "B=4 S=1000", "factored D=256 B=2 S=2048"], "norm_rope": ["B=1 S=8192", "B=4 S=2048"]}), flush=True)
+                      "attention": "B=1 S=4096 causal", "general": ["B=1 S=2048", "B=4 S=1000", "factored D=256 B=2 S=2048"], "norm_rope": [f"B={b} S={s}" for b, s in SWEEP]}), flush=True)
 
 
 def main():
@@ -339,11 +373,16 @@ def main():
                      / MFMA_BF16_PEAK_TFS,
                      "frac_step_wall": head["tflops"] / MFMA_BF16_PEAK_TFS,
                      "frac_note": "frac: attention kernel alone (graph-replay events); frac_step_*: the whole "
-                                  "step (K-prep launch + attention) by device events / by the host clock"},
+                                  "step (K-prep launch + attention, K steps replayed as one HIP graph) by "
+                                  "device events / by the host clock"},
         "kernels": {"attention_us": head["attention_kernel_us"],
                     "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
                     "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows (one launch)",
-                    "device_ms_per_step": head["device_ms_per_step"], "settle_steps": head["settle_steps"]},
+                    "device_ms_per_step": head["device_ms_per_step"], "settle_steps": head["settle_steps"],
+                    "step_timing": "K steps recorded once into a HIP graph and replayed (host clock around "
+                                   "the replay, synchronised on both sides)",
+                    "eager_ms_per_step": head["eager_ms_per_step"],
+                    "eager_device_ms_per_step": head["eager_device_ms_per_step"]},
     }
     if not args.quick:
         line["norm_rope"] = norm_rope_sweep(args, torch, kf)

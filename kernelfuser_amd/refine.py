@@ -110,9 +110,10 @@ def _rope(x, cos, sin):
     return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], dim=-1)
 
 
-def reference_fp32(xs, causal: bool, rotary: bool) -> torch.Tensor:
-    """FP32 RMSNorm (+ RoPE) and FP32 softmax attention with scale D^-1/2, one
-    KV head's query-head group at a time; returns FP32 [B,Hq,S,D]."""
+def reference_fp32(xs, causal: bool, rotary: bool, scale: float | None = None) -> torch.Tensor:
+    """FP32 RMSNorm (+ RoPE) and FP32 softmax attention with scale ``scale``
+    (default D^-1/2), one KV head's query-head group at a time; returns FP32
+    [B,Hq,S,D]."""
     q, k, v, gq, gk, cos, sin = xs
     b, hq, s, d = q.shape
     hkv = k.shape[1]
@@ -125,7 +126,7 @@ def reference_fp32(xs, causal: bool, rotary: bool) -> torch.Tensor:
     for j in range(hkv):
         qg = qn[:, j * grp:(j + 1) * grp]                      # [B,G,S,D]
         kt = kn[:, j:j + 1].transpose(-1, -2).contiguous()     # [B,1,D,S]
-        sc = torch.matmul(qg, kt) * (d ** -0.5)
+        sc = torch.matmul(qg, kt) * (d ** -0.5 if scale is None else scale)
         if mask is not None:
             sc = sc.masked_fill(mask, float("-inf"))
         out[:, j * grp:(j + 1) * grp] = torch.matmul(torch.softmax(sc, dim=-1), v[:, j:j + 1].float())
