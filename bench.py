@@ -217,7 +217,8 @@ def prefill_shapes(args, torch, kf):
         ms = time_graph(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
                                                        bn=64, kn=kn, norm_style=args.norm_style), 20)
         f = kf.attention_flops(b, hq, s, d, True)
-        rows.append({"B": b, "S": s, "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
+        rows.append({"B": b, "S": s, "kernel": kf._lib.attention_kernel(b, hq, hkv, s, d, True, kf._lib.MODE_QUERY),
+                     "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
                      "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS})
         del xs, out, kn
     return rows

@@ -49,9 +49,10 @@ with its bootstrap 95% interval; the by-shape choice is ``kept`` when it is
 the fastest or when that interval reaches 1.0 or its median is within 1%.
 
 ``python -m kernelfuser_amd.refine --grid tune --out tune.json`` runs the
-reference's twelve shapes plus this build's configurations (B=4 S=1000 first)
-and shapes beside the ping-pong and split thresholds; the norm+RoPE sweep's
-six shapes then run the preparation arms only.
+reference's twelve shapes plus this build's configurations (B=4 S=1000 first;
+in the refinement inputs' rounding style and again in the FP32 style that
+bench.py times) and shapes beside the ping-pong and split thresholds; the
+norm+RoPE sweep's six shapes then run the preparation arms only.
 """
 from __future__ import annotations
 
@@ -85,7 +86,12 @@ THRESHOLD_SHAPES = [
 # sweep; the causal flag is unused): preparation arms only
 PREPARE_SHAPES = [("Qwen3-8B", b, s, False, True, "prepare") for b, s in
                   ((1, 512), (1, 2048), (1, 8192), (4, 2048), (8, 1024), (16, 512))]
-SHAPES = CONFIG_SHAPES + THRESHOLD_SHAPES + REFERENCE_SHAPES + PREPARE_SHAPES
+# the configurations again in the FP32 rounding style that bench.py times,
+# and causal grids of 8-15 query blocks that the persistent pairing fills
+CONFIG_FP32_SHAPES = [r + ("fp32",) for r in CONFIG_SHAPES] + [("Qwen3-8B", 1, 3072, True, True, "fp32")]
+PAIRING_SHAPES = [("Qwen3-8B", b, s, True, True, st) for b, s in ((8, 1024), (4, 1536), (16, 1024))
+                  for st in ("fp32", "hf")]
+SHAPES = CONFIG_SHAPES + CONFIG_FP32_SHAPES + THRESHOLD_SHAPES + PAIRING_SHAPES + REFERENCE_SHAPES + PREPARE_SHAPES
 TUNE_SEED = 32109  # rope:808
 
 # decision -> option arms (each option arm forces one alternative)
@@ -284,15 +290,17 @@ def prepared_fp32(xs, rotary: bool) -> torch.Tensor:
 
 
 def tune_row(model: str, b: int, s: int, causal: bool, rotary: bool, prepare_only: bool = False, *, rounds=3,
-             samples=5, launches=20, settle_ms: float = 150.0, device="cuda:0") -> dict:
+             samples=5, launches=20, settle_ms: float = 150.0, style: str | None = None, device="cuda:0") -> dict:
     """One shape: gate and evidence for every arm, interleaved timing,
     decisions.  ``prepare_only``: the preparation arms alone, in the FP32
-    style of the isolated norm+RoPE workload."""
+    style of the isolated norm+RoPE workload.  ``style``: the rounding style
+    of every arm (default: refine.build_arms' choice)."""
     xs = refinement_inputs(model, b, s, SEEDS[0], rotary, device)
     ref = None if prepare_only else reference_fp32(xs, causal, rotary)
     ref_prep = prepared_fp32(xs, rotary)
     specs = arm_specs(model, s, causal, rotary, prepare_only)
-    arms = build_tuning_arms(xs, specs, causal, rotary, "fp32" if prepare_only else None)
+    style = "fp32" if prepare_only else style
+    arms = build_tuning_arms(xs, specs, causal, rotary, style)
     checks = {}
     for name, call in list(arms.items()):
         try:
@@ -313,7 +321,7 @@ def tune_row(model: str, b: int, s: int, causal: bool, rotary: bool, prepare_onl
             del arms[name]
     del ref, ref_prep
     row = {"model": model, "shape": [b, s, causal], "rotary": rotary, "geometry": list(MODELS[model]),
-           "prepare_only": prepare_only, "correctness": checks}
+           "prepare_only": prepare_only, "style": style or ("hf" if rotary else "legacy"), "correctness": checks}
     if any(not c["pass"] for c in checks.values()):
         row["status"] = "failed_gate"  # every alternative offered here must run and pass
         return row
@@ -353,7 +361,7 @@ def run(rows, *, launches: int = 20, rounds: int = 3, samples: int = 5, save=Non
             for model, b, s, causal, rotary, *kind in rows:
                 t0 = time.time()
                 row = tune_row(model, b, s, causal, rotary, kind == ["prepare"], rounds=rounds, samples=samples,
-                               launches=launches)
+                               launches=launches, style=kind[0] if kind and kind[0] in ("fp32", "hf", "legacy") else None)
                 exclusive.guarded(row, mon.between(t0, time.time()))
                 rec["rows"].append(row)
                 if save:

@@ -134,7 +134,10 @@ def test_attention_kernel_query(lib):
     assert k(1, 64, 8, 2048, 128, True, 0) == "pingpong"    # Qwen3-32B: the pairing fills every CU
     assert k(1, 32, 8, 2048, 128, False, 0) == "pingpong"   # 256 items: one round
     assert k(1, 32, 8, 3072, 128, False, 0) == "general"    # 384 items: 1.5 rounds
-    assert k(4, 32, 8, 1000, 128, True, 0) == "general"     # 8 blocks
+    assert k(4, 32, 8, 1000, 128, True, 0) == "pingpong"    # 8 blocks, one paired unit per CU
+    assert k(8, 32, 8, 1024, 128, True, 0) == "general"     # 8 blocks, two paired units per CU
+    assert k(4, 32, 8, 1000, 128, False, 0) == "general"    # 8 blocks, not causal
+    assert k(1, 32, 8, 1024, 128, True, 0) == "general"     # 8 blocks, not paired
     assert k(1, 32, 8, 8192, 128, True, 2) == "general"     # mode 'full'
     assert k(1, 16, 8, 8192, 256, True, 0) == "general"     # D = 256
     assert k(1, 40, 8, 8192, 128, True, 0) == "general"     # odd GQA ratio
@@ -142,6 +145,7 @@ def test_attention_kernel_query(lib):
         assert k(4, 32, 8, 1000, 128, True, 0) == "wide"
     with _lib.tuning(persistent=1):
         assert k(1, 64, 8, 2048, 128, True, 0) == "general"  # without the pairing the grid does not fill
+        assert k(4, 32, 8, 1000, 128, True, 0) == "general"
     assert lib.kfmi_attention_kernel(1, 32, 8, 0, 128, 1, 0) == -EINVAL
     assert lib.kfmi_attention_kernel(1, 32, 8, 16, 128, 1, 7) == -EINVAL
     with _lib.tuning(attn_kernel="pingpong"):

@@ -9,8 +9,8 @@ instead of another head's finite rows.  A tile copy that read past its
 descriptor would put 0 * NaN into P.V and the stored rows would be NaN.  The
 guard is allocated memory, so no variant of the kernels can fault here.
 
-Shapes: the general kernel's ragged grids (B=4 S=1000, S=33, S=129), the
-ping-pong kernel's (S=2970, S=3200), D=256 with the split-KV plan (S=1900,
+Shapes: the general kernel's ragged grids (S=33, S=129, and B=4 S=1000
+forced onto it), the ping-pong kernel's (B=4 S=1000, S=2970, S=3200), D=256 with the split-KV plan (S=1900,
 Gemma-3-12B heads), mode 'full' (raw K tiles) and the factored path.
 """
 import pytest
@@ -18,7 +18,7 @@ import torch
 
 import oracle
 from helpers import announce
-from kernelfuser_amd import GEMMA3_12B, QWEN3_8B, launch_attention, launch_factored_attention, make_inputs
+from kernelfuser_amd import GEMMA3_12B, QWEN3_8B, _lib, launch_attention, launch_factored_attention, make_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -46,9 +46,10 @@ def _check(out, ref_fn, s):
     assert m["pass"], m
 
 
-@pytest.mark.parametrize("b,s", [(4, 1000), (1, 33), (1, 129), (1, 2970), (1, 3200)])
+@pytest.mark.parametrize("b,s,kernel", [(4, 1000, "auto"), (4, 1000, "general"), (1, 33, "auto"), (1, 129, "auto"),
+                                          (1, 2970, "auto"), (1, 3200, "auto")])
 @pytest.mark.parametrize("mode", ["query", "full"])
-def test_qwen3_ragged_tiles_read_zeros(gpu, b, s, mode):
+def test_qwen3_ragged_tiles_read_zeros(gpu, b, s, kernel, mode):
     xs = make_inputs(b, s, QWEN3_8B, 4949)
     q = xs.q.to(gpu)
     k = guarded(xs.k, gpu)
@@ -57,8 +58,9 @@ def test_qwen3_ragged_tiles_read_zeros(gpu, b, s, mode):
     gq, gk = xs.gq.to(gpu), xs.gk.to(gpu)
     kn = guarded(torch.zeros_like(xs.k), gpu)
     out = torch.full_like(q, float("nan"))
-    announce(f"guard {mode} fp32 B={b} S={s} causal")
-    launch_attention((q, k, v, gq, gk, cos, sin), out, causal=True, mode=mode, kn=kn, norm_style="fp32")
+    announce(f"guard {mode} fp32 B={b} S={s} causal kernel={kernel}")
+    with _lib.tuning(attn_kernel=kernel):
+        launch_attention((q, k, v, gq, gk, cos, sin), out, causal=True, mode=mode, kn=kn, norm_style="fp32")
     torch.cuda.synchronize()
     _check(out, lambda rows: oracle.oracle_rows_fp32(*xs.astuple(), rows, True), s)
 

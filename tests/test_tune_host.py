@@ -25,6 +25,7 @@ def test_arms_follow_geometry():
     assert tune.SHAPES[0] == ("Qwen3-8B", 4, 1000, True, True)
     assert len(tune.REFERENCE_SHAPES) == 12  # rope:776
     assert all(r[-1] == "prepare" for r in tune.PREPARE_SHAPES) and len(tune.PREPARE_SHAPES) == 6
+    assert all(r[-1] == "fp32" for r in tune.CONFIG_FP32_SHAPES) and len(tune.CONFIG_FP32_SHAPES) == 6
 
 
 def test_dispatch_matches():
