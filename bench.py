@@ -99,6 +99,19 @@ def load_traffic():
         return {}
 
 
+NOMINAL_GHZ = 2.4  # MI355X peak engine clock, at which MFMA_BF16_PEAK_TFS is quoted
+
+
+def clock_of(kf, fn, launches=200):
+    """Shader clock during `fn`'s attention launches: `launches` back-to-back
+    calls with per-workgroup clock stamps on (kfmi_clock_stamps), summarised
+    over the last launch's workgroups; results are unchanged by the stamps."""
+    with kf._lib.tuning(clock_stamps=1):
+        for _ in range(launches):
+            fn()
+    return kf._lib.clock_summary(kf._lib.clock_stamps())
+
+
 def headline(args, torch, kf):
     """Timed steps of launch_attention(mode='query') plus the attention kernel alone."""
     b, s = args.batch, args.seq
@@ -171,6 +184,8 @@ def headline(args, torch, kf):
     prep_ms = time_graph(lambda i: kf.prepare_attention(xs.reference7, None, kn, only_k=True, rope=True,
                                                         norm_style=args.norm_style), 100)
     res["attention_kernel_us"] = attn_ms * 1e3
+    res["clock"] = clock_of(kf, lambda: kf.attention_prefill(xs.q, kn, xs.v, out, gq=xs.gq, cos=xs.cos, sin=xs.sin,
+                                                              causal=True, fuse_q=True, norm_style=args.norm_style))
     res["prep_kernel_us"] = prep_ms * 1e3
     res["attention_kernel_tflops"] = flops / (attn_ms * 1e-3) / 1e12
     prep_bytes = kf.k_prep_bytes(b, hkv, s, d)
@@ -214,12 +229,15 @@ def prefill_shapes(args, torch, kf):
     for b, s in [(1, 2048), (1, 8192), (4, 1000)]:
         xs = kf.make_inputs(b, s, QWEN3_8B, 2909).to("cuda:0")
         out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
-        ms = time_graph(lambda i: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128,
-                                                       bn=64, kn=kn, norm_style=args.norm_style), 20)
+        step = lambda: kf.launch_attention(xs.reference7, out, causal=True, mode="query", bm=128, bn=64, kn=kn,
+                                           norm_style=args.norm_style)
+        ms = time_graph(lambda i: step(), 20)
         f = kf.attention_flops(b, hq, s, d, True)
+        ghz = clock_of(kf, step)["ghz_median"]
         rows.append({"B": b, "S": s, "kernel": kf._lib.attention_kernel(b, hq, hkv, s, d, True, kf._lib.MODE_QUERY),
                      "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
-                     "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS})
+                     "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, "clock_ghz": ghz,
+                     "frac_mfma_at_clock": f / (ms * 1e-3) / 1e12 / (MFMA_BF16_PEAK_TFS * ghz / NOMINAL_GHZ)})
         del xs, out, kn
     return rows
 
@@ -230,11 +248,14 @@ def factored(args, torch, kf):
     xs = kf.make_inputs(b, s, GEMMA3_12B, 1909, rope=False).to("cuda:0")
     out, kn = torch.empty_like(xs.q), torch.empty_like(xs.k)
     inv = torch.empty(xs.q.shape[:-1], device="cuda:0", dtype=torch.float32)
-    ms = time_graph(lambda i: kf.launch_factored_attention((xs.q, xs.k, xs.v, xs.gq, xs.gk), out, inv, kn,
-                                                           causal=True, bm=128, bn=64), 20)
+    step = lambda: kf.launch_factored_attention((xs.q, xs.k, xs.v, xs.gq, xs.gk), out, inv, kn, causal=True, bm=128,
+                                                bn=64)
+    ms = time_graph(lambda i: step(), 20)
     f = kf.attention_flops(b, hq, s, d, True)
+    ghz = clock_of(kf, step)["ghz_median"]
     return {"B": b, "S": s, "Hq": hq, "Hkv": hkv, "D": d, "causal": True, "us": ms * 1e3,
-            "tflops": f / (ms * 1e-3) / 1e12, "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS}
+            "tflops": f / (ms * 1e-3) / 1e12, "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS,
+            "clock_ghz": ghz, "frac_mfma_at_clock": f / (ms * 1e-3) / 1e12 / (MFMA_BF16_PEAK_TFS * ghz / NOMINAL_GHZ)}
 
 
 def cpu_baseline(args, torch, xs_cpu, out_gpu):
@@ -375,7 +396,14 @@ def main():
                      "frac_step_wall": head["tflops"] / MFMA_BF16_PEAK_TFS,
                      "frac_note": "frac: attention kernel alone (graph-replay events); frac_step_*: the whole "
                                   "step (K-prep launch + attention, K steps replayed as one HIP graph) by "
-                                  "device events / by the host clock"},
+                                  "device events / by the host clock",
+                     "clock": dict(head["clock"], nominal_ghz=NOMINAL_GHZ,
+                                   peak_at_clock=MFMA_BF16_PEAK_TFS * head["clock"]["ghz_median"] / NOMINAL_GHZ,
+                                   frac_at_clock=head["attention_kernel_tflops"]
+                                   / (MFMA_BF16_PEAK_TFS * head["clock"]["ghz_median"] / NOMINAL_GHZ),
+                                   note="shader clock of the attention kernel's workgroups (per-workgroup "
+                                        "s_memtime / s_memrealtime stamps, 200 back-to-back launches, last "
+                                        "launch); peak_at_clock scales the 2.5 PFLOP/s peak to that clock")},
         "kernels": {"attention_us": head["attention_kernel_us"],
                     "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
                     "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows (one launch)",

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 8
+#define KFMI_ABI_VERSION 9
 
 /* status codes */
 #define KFMI_OK 0
@@ -106,6 +106,8 @@ typedef struct {
   int32_t split;       /* general kernel at D = 256: 1 never splits a query block's key range */
   int32_t persistent;  /* ping-pong and wide kernels: 1 = one work item per workgroup (no
                           persistent long/short pairing) */
+  int32_t clock_stamps; /* 1 = attention launches record per-workgroup clock stamps
+                           (kfmi_clock_stamps); results are unchanged */
 } kfmi_tuning;
 
 /* Set (t != NULL) or clear (t == NULL) the calling thread's overrides.
@@ -115,6 +117,27 @@ int kfmi_set_tuning(const kfmi_tuning *t);
 
 /* The calling thread's current overrides (all zero unless set). */
 void kfmi_get_tuning(kfmi_tuning *out);
+
+/* Clock stamps of one attention workgroup: the shader-clock counter
+ * (s_memtime) and the 100 MHz real-time counter (s_memrealtime), read by the
+ * workgroup's first thread when it starts (t0, r0) and when it ends (t1, r1).
+ * (t1 - t0) / (r1 - r0) * 100 MHz is the workgroup's average shader clock. */
+typedef struct {
+  uint64_t t0, t1, r0, r1;
+} kfmi_clock_stamp;
+
+#define KFMI_CLOCK_STAMPS_MAX 2048 /* workgroups past this record none */
+
+/* Stamps of the last attention launch that recorded them (kfmi_tuning
+ * .clock_stamps = 1) on the current device: waits for the device, copies up
+ * to `max` entries (one per workgroup, in workgroup order) into `out` (may be
+ * NULL when max is 0) and returns how many that launch recorded (0 before
+ * any), or -KFMI_EINVAL / -KFMI_EDEVICE / -KFMI_ELAUNCH.  Every recording launch on a GPU writes that GPU's one static array
+ * (KFMI_CLOCK_STAMPS_MAX entries, held until the process ends), so launches
+ * that record at the same time on one GPU race on it.  No counterpart in the
+ * reference: it measures the clock that bounds a kernel's MFMA rate, which
+ * the GPU lowers under power limits. */
+int kfmi_clock_stamps(kfmi_clock_stamp *out, int max);
 
 /* Row preparation: per-(token,head) RMSNorm(eps) * gamma, then optional
  * rotate-half RoPE, BF16 out.  Replaces prepare_attention -> prepare_kernel

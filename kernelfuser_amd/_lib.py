@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -82,6 +82,8 @@ def load() -> ctypes.CDLL:
         lib.kfmi_set_tuning.argtypes = [ctypes.POINTER(Tuning)]
         lib.kfmi_get_tuning.restype = None
         lib.kfmi_get_tuning.argtypes = [ctypes.POINTER(Tuning)]
+        lib.kfmi_clock_stamps.restype = ctypes.c_int
+        lib.kfmi_clock_stamps.argtypes = [ctypes.POINTER(ClockStamp), _I]
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
@@ -114,7 +116,41 @@ class Tuning(ctypes.Structure):
     """kfmi_tuning of include/kfmi.h: dispatch choices the library otherwise
     makes by shape (0 = by shape)."""
     _fields_ = [("attn_kernel", ctypes.c_int32), ("pp_heads", ctypes.c_int32), ("rows_heads", ctypes.c_int32),
-                ("split", ctypes.c_int32), ("persistent", ctypes.c_int32)]
+                ("split", ctypes.c_int32), ("persistent", ctypes.c_int32), ("clock_stamps", ctypes.c_int32)]
+
+
+class ClockStamp(ctypes.Structure):
+    """kfmi_clock_stamp of include/kfmi.h."""
+    _fields_ = [("t0", ctypes.c_uint64), ("t1", ctypes.c_uint64), ("r0", ctypes.c_uint64), ("r1", ctypes.c_uint64)]
+
+
+CLOCK_STAMPS_MAX = 2048
+REALTIME_HZ = 100e6  # s_memrealtime
+
+
+def clock_stamps() -> list[tuple[int, int, int, int]]:
+    """(t0, t1, r0, r1) per workgroup of the last attention launch on the
+    current device that recorded clock stamps (kfmi_clock_stamps; launches
+    record them under ``tuning(clock_stamps=1)``).  Waits for the device."""
+    lib = load()
+    buf = (ClockStamp * CLOCK_STAMPS_MAX)()
+    n = lib.kfmi_clock_stamps(buf, CLOCK_STAMPS_MAX)
+    if n < 0:
+        raise RuntimeError(f"kfmi_clock_stamps: {lib.kfmi_last_error().decode(errors='replace')}")
+    return [(r.t0, r.t1, r.r0, r.r1) for r in buf[:n]]
+
+
+def clock_summary(stamps) -> dict:
+    """Shader clock per workgroup, (t1 - t0) / (r1 - r0) x 100 MHz, in GHz
+    (median, min, max), the workgroups' median lifetime and the span from the
+    first start to the last end (microseconds)."""
+    ghz = sorted((t1 - t0) / (r1 - r0) * REALTIME_HZ / 1e9 for t0, t1, r0, r1 in stamps if r1 > r0)
+    if not ghz:
+        raise ValueError("no clock stamps")
+    life = sorted((r1 - r0) / REALTIME_HZ * 1e6 for _, _, r0, r1 in stamps)
+    span = (max(r1 for *_, r1 in stamps) - min(r0 for _, _, r0, _ in stamps)) / REALTIME_HZ * 1e6
+    return {"ghz_median": ghz[len(ghz) // 2], "ghz_min": ghz[0], "ghz_max": ghz[-1], "workgroups": len(stamps),
+            "workgroup_us_median": life[len(life) // 2], "span_us": span}
 
 
 TUNING_FIELDS = tuple(f for f, _ in Tuning._fields_)

@@ -38,6 +38,7 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE];
 
+  clock_stamp<false>(p.stamps);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -245,6 +246,7 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
       __syncthreads();  // the K/V buffers become the epilogue's staging tiles
       store_rows_lds<D>(smem + w * (32 * 2 * D), p.out + qoff * D, q0, S, lane, sm.l_run, o);
     }
+    clock_stamp<true>(p.stamps);
     return;
   }
   // ---- one half of a split query block: publish the partial state (O
@@ -291,7 +293,10 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  if (arrived_before == 0) return;  // the other half merges
+  if (arrived_before == 0) {  // the other half merges
+    clock_stamp<true>(p.stamps);
+    return;
+  }
   // Merge in fixed (first half, second half) operand order, whichever half
   // runs it, with explicit fmaf, so the result does not depend on timing.
   const float mo = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(other, (NQ * 1024 + tid) * 4, 0, SC1));
@@ -316,6 +321,7 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   __syncthreads();
   store_rows_lds<D>(smem + w * (32 * 2 * D), p.out + qoff * D, q0, S, lane, fmaf(l0, a0, l1 * a1), o);
   if (tid == 0) atomicExch(p.counters + pair, 0);
+  clock_stamp<true>(p.stamps);
 }
 
 template <int D, int BN, bool CAUSAL, int PRO, int ST, bool FK>
@@ -562,6 +568,7 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
   p.slot2 = 0;
   p.counters = nullptr;
   p.partials = nullptr;
+  p.stamps = nullptr;
   p.q = a.q; p.k = a.k; p.v = a.v; p.gq = a.gq; p.cos = a.cos; p.sin = a.sin;
   p.gk = a.gk;
   p.out = a.out; p.inv = a.inv;
@@ -618,6 +625,13 @@ hipError_t launch_attention(const AttnArgs &a, hipStream_t stream) {
     const int64_t cus = device_cus();
     if (a.causal && a.D == 128 && p.n_items == 0 && cus % nbh == 0 && blocks > cus && blocks <= 2 * cus)
       p.slot2 = (int)cus;
+  }
+  if (tun.clock_stamps) {
+    void *st = nullptr;
+    const hipError_t se = clock_stamp_buffer(&st);
+    if (se != hipSuccess) return se;
+    p.stamps = (unsigned long long *)st;
+    clock_stamps_recorded(blocks);
   }
   hipError_t e;
   if (a.D == 128) {

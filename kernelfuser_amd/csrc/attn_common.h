@@ -118,8 +118,24 @@ struct AttnParams {
   int16_t it_qb[128], it_t0[128], it_t1[128], it_sid[128];
   int *counters;
   float *partials;
+  // 4 * KFMI_CLOCK_STAMPS_MAX words of clock stamps, or NULL (no stamps)
+  unsigned long long *stamps;
 };
 constexpr int MAX_SPLIT_ITEMS = 128;
+
+// Clock stamps {t0, t1, r0, r1} of workgroup blockIdx.x (kfmi_clock_stamp):
+// the shader-clock counter and the 100 MHz real-time counter, read by the
+// first thread at the workgroup's start (END = false) and at each of its
+// exits (END = true).  Vector stores to a device array; nothing when the
+// launch passes no array.
+template <bool END>
+__device__ __forceinline__ void clock_stamp(unsigned long long *st) {
+  if (st != nullptr && threadIdx.x == 0 && blockIdx.x < KFMI_CLOCK_STAMPS_MAX) {
+    unsigned long long *e = st + 4 * blockIdx.x;
+    e[END ? 1 : 0] = __builtin_amdgcn_s_memtime();
+    e[END ? 3 : 2] = __builtin_amdgcn_s_memrealtime();
+  }
+}
 
 namespace {
 

@@ -29,6 +29,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE + (STAGE_TAB ? 2 * TAB_BYTES : 0)];
 
+  clock_stamp<false>(p.stamps);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0..7
@@ -256,6 +257,7 @@ __global__ __launch_bounds__(512, 1) void attn_pp_kernel(AttnParams p) {
     run(qb, kvi, j);
     __syncthreads();  // the next item refills the LDS buffers
   }
+  clock_stamp<true>(p.stamps);
 }
 
 template <bool CAUSAL, int PRO, int ST, bool VT>

@@ -245,6 +245,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE + (STAGE_TAB ? 2 * TAB_BYTES : 0)];
 
+  clock_stamp<false>(p.stamps);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // the wave's head within the item
@@ -671,6 +672,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     run(qb, kvi, jq);
     __syncthreads();  // the next item refills the LDS buffers
   }
+  clock_stamp<true>(p.stamps);
 }
 
 template <bool CAUSAL, int PRO, int ST>

@@ -170,6 +170,8 @@ int kfmi_set_tuning(const kfmi_tuning *t) {
     return fail(KFMI_EINVAL, "rows_heads must be 0, 2 or 4 (got %d)", t->rows_heads);
   if (t->split < 0 || t->split > 1) return fail(KFMI_EINVAL, "split must be 0 or 1 (got %d)", t->split);
   if (t->persistent < 0 || t->persistent > 1) return fail(KFMI_EINVAL, "persistent must be 0 or 1 (got %d)", t->persistent);
+  if (t->clock_stamps < 0 || t->clock_stamps > 1)
+    return fail(KFMI_EINVAL, "clock_stamps must be 0 or 1 (got %d)", t->clock_stamps);
   g_tuning = *t;
   g_error.clear();
   return KFMI_OK;
@@ -177,6 +179,22 @@ int kfmi_set_tuning(const kfmi_tuning *t) {
 
 void kfmi_get_tuning(kfmi_tuning *out) {
   if (out) *out = g_tuning;
+}
+
+int kfmi_clock_stamps(kfmi_clock_stamp *out, int max) {
+  if (max < 0 || (max > 0 && out == nullptr)) return -fail(KFMI_EINVAL, "kfmi_clock_stamps: out is NULL or max < 0");
+  if (const int rc = check_device()) return -rc;
+  const int n = kfmi::clock_stamps_count();
+  const int m = n < max ? n : max;
+  if (m > 0) {
+    void *src = nullptr;
+    hipError_t e = kfmi::clock_stamp_buffer(&src);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(out, src, (size_t)m * sizeof(kfmi_clock_stamp), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return -fail(KFMI_ELAUNCH, "kfmi_clock_stamps: %s", hipGetErrorString(e));
+  }
+  g_error.clear();
+  return n;
 }
 
 int kfmi_last_launches(kfmi_launch_info *out, int max) {

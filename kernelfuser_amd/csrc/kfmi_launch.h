@@ -95,4 +95,12 @@ hipError_t noalloc_scratch(void **addr);
 // with a fill kernel.
 hipError_t clear_scratch_words(void *addr, int64_t bytes, hipStream_t stream);
 
+// Device address of the current device's static clock-stamp array
+// (4 * KFMI_CLOCK_STAMPS_MAX 64-bit words; taken once per device with
+// hipGetSymbolAddress and cached), and the number of entries the last
+// recording launch on each device wrote.
+hipError_t clock_stamp_buffer(void **addr);
+void clock_stamps_recorded(int64_t workgroups);
+int clock_stamps_count();
+
 }  // namespace kfmi

@@ -25,6 +25,11 @@ namespace {
 
 static __device__ __align__(256) unsigned char scratch[KFMI_SCRATCH_BYTES];
 
+// Clock stamps of the attention launches that record them: {t0, t1, r0, r1}
+// per workgroup (kfmi_clock_stamp), one array per GPU, written only by the
+// launches that pass its address.
+static __device__ __align__(256) unsigned long long clock_stamps[4 * KFMI_CLOCK_STAMPS_MAX];
+
 // Fill n 32-bit words with zeros (one workgroup; n is a few hundred).  A
 // kernel rather than hipMemsetAsync, so that a capturing caller records an
 // ordinary kernel node.
@@ -35,24 +40,45 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t *p, int n) {
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void *g_addr[kMaxDevices];  // device address of `scratch` per device ordinal (nullptr: not taken yet)
+void *g_stamp_addr[kMaxDevices];  // device address of `clock_stamps` per device ordinal
+int g_stamp_count[kMaxDevices];   // entries written by the last recording launch per device
 
-}  // namespace
-
-hipError_t noalloc_scratch(void **addr) {
+// Address of `sym` on the current device, cached in cache[device].
+hipError_t symbol_address(const void *sym, void **cache, void **addr) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_mu);
-  if (g_addr[dev] == nullptr) {
+  if (cache[dev] == nullptr) {
     void *p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    e = hipGetSymbolAddress(&p, sym);
     if (e != hipSuccess) return e;
     if (p == nullptr) return hipErrorInvalidSymbol;
-    g_addr[dev] = p;
+    cache[dev] = p;
   }
-  *addr = g_addr[dev];
+  *addr = cache[dev];
   return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t noalloc_scratch(void **addr) { return symbol_address(HIP_SYMBOL(scratch), g_addr, addr); }
+
+hipError_t clock_stamp_buffer(void **addr) { return symbol_address(HIP_SYMBOL(clock_stamps), g_stamp_addr, addr); }
+
+void clock_stamps_recorded(int64_t workgroups) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return;
+  std::lock_guard<std::mutex> lock(g_mu);
+  g_stamp_count[dev] = (int)(workgroups < KFMI_CLOCK_STAMPS_MAX ? workgroups : KFMI_CLOCK_STAMPS_MAX);
+}
+
+int clock_stamps_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  std::lock_guard<std::mutex> lock(g_mu);
+  return g_stamp_count[dev];
 }
 
 hipError_t clear_scratch_words(void *addr, int64_t bytes, hipStream_t stream) {

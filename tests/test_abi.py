@@ -27,7 +27,7 @@ def lib():
 def test_header_declares_the_bound_entry_points():
     names = _declared()
     queries = {"kfmi_abi_version", "kfmi_last_error", "kfmi_attention_workspace_bytes", "kfmi_last_launches",
-               "kfmi_set_tuning", "kfmi_get_tuning", "kfmi_attention_kernel"}
+               "kfmi_set_tuning", "kfmi_get_tuning", "kfmi_attention_kernel", "kfmi_clock_stamps"}
     assert queries <= set(names)
     assert set(_lib.SIGNATURES) == set(names) - queries
 
@@ -184,7 +184,8 @@ def test_tuning_overrides_validate_and_scope(lib):
     thread, and a forced kernel that cannot run a shape fails the call with
     KFMI_EINVAL before any device access."""
     assert _lib.get_tuning() == dict.fromkeys(_lib.TUNING_FIELDS, 0)
-    for bad in ({"attn_kernel": 4}, {"pp_heads": 3}, {"rows_heads": 1}, {"split": 2}, {"persistent": -1}):
+    for bad in ({"attn_kernel": 4}, {"pp_heads": 3}, {"rows_heads": 1}, {"split": 2}, {"persistent": -1},
+                {"clock_stamps": 2}):
         with pytest.raises(ValueError):
             _lib.set_tuning(**bad)
     assert _lib.get_tuning() == dict.fromkeys(_lib.TUNING_FIELDS, 0)
@@ -204,6 +205,21 @@ def test_tuning_overrides_validate_and_scope(lib):
     with _lib.tuning(attn_kernel="pingpong"):
         assert lib.kfmi_attention_bf16(*args256) == EINVAL
     assert _lib.get_tuning()["attn_kernel"] == 0
+
+
+def test_clock_stamp_layout_and_arguments(lib):
+    """kfmi_clock_stamp and kfmi_tuning sizes match the header's fields;
+    kfmi_clock_stamps rejects a NULL buffer with room for entries."""
+    assert ctypes.sizeof(_lib.ClockStamp) == 32
+    assert ctypes.sizeof(_lib.Tuning) == 4 * 6
+    m = re.search(r"#define KFMI_CLOCK_STAMPS_MAX (\d+)", HEADER.read_text())
+    assert int(m.group(1)) == _lib.CLOCK_STAMPS_MAX
+    assert lib.kfmi_clock_stamps(None, 4) == -EINVAL
+    assert "NULL" in _err(lib)
+    s = [(0, 2000, 0, 100), (0, 4200, 10, 110), (5, 1805, 20, 120)]  # 2.0, 4.2, 1.8 GHz
+    c = _lib.clock_summary(s)
+    assert (round(c["ghz_median"], 6), round(c["ghz_min"], 6), round(c["ghz_max"], 6)) == (2.0, 1.8, 4.2)
+    assert c["workgroups"] == 3 and c["workgroup_us_median"] == 1.0 and round(c["span_us"], 6) == 1.2
 
 
 def test_launch_handle_reads_only_its_own_call():
