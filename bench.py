@@ -329,8 +329,9 @@ def pmc_run(torch, kf):
     for _ in range(3):
         kf.launch_factored_attention((fx.q, fx.k, fx.v, fx.gq, fx.gk), fo, finv, fk, causal=True, bm=128, bn=64)
     del fx, fo, fk, finv
-    # norm+RoPE: the six sweep shapes, in the sweep's order (the three B=1
-    # shapes run two heads per workgroup, the three 170 MB ones four)
+    # norm+RoPE: the six sweep shapes, in the sweep's order (B=1 S=512 and
+    # S=8192 run two heads per workgroup, B=1 S=2048 and the three 170 MB
+    # shapes four)
     for b, s in SWEEP:
         nr = kf.make_inputs(b, s, QWEN3_8B, 1909, with_v=False).to("cuda:0")
         qn, kn2 = torch.empty_like(nr.q), torch.empty_like(nr.k)

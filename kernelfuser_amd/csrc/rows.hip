@@ -125,12 +125,14 @@ __device__ __forceinline__ float row_sum(float x) {
 #endif
 // Heads per workgroup (rows per lane) of rows_kernel: two, or four for Q+K
 // launches at D = 128 where the tuning runner measured four faster:
-// - FP32 style, at least 2^18 rows with S <= 4096: 27.2 vs 28.1-28.4 us at
-//   the 170 MB shapes (B >= 4), a tie at B = 1, S = 2048 and S = 8192;
-// - HF and legacy styles, whose per-row arithmetic is longer, from 2^15 to
-//   2^17 rows: 8.2 vs 9.9 us at B = 1, S = 2048 (16-21% from 40k to 82k rows,
-//   3-5% at 123k-164k), while two heads are 1-3% faster at 160k rows and
-//   more.
+// - every style from 2^15 to 2^17 rows: HF and legacy, whose per-row
+//   arithmetic is longer, 8.2 vs 9.9 us at B = 1, S = 2048 (16-21% from 40k
+//   to 82k rows, 3-5% at 123k-164k); FP32 8.56-8.68 vs 8.97-9.20 us at
+//   B = 1, S = 2048 (82k rows; two tuning rows) and 12.1 vs 12.3 us at
+//   S = 3072, while two heads are 1-3% faster at 160k rows and more
+//   (FP32 B = 1, S = 4096: 15.2 vs 15.5 us);
+// - FP32 style, also at least 2^18 rows with S <= 4096: 27.2 vs 28.1-28.4
+//   us at the 170 MB shapes (B >= 4), a tie at S = 8192.
 // Fewer, longer workgroups lose on small launches (below 2^15 rows), and
 // the K-only preparation is faster with two.
 constexpr int ROWS_HPW = 2, ROWS_HPW_BIG = 4;
@@ -352,8 +354,8 @@ hipError_t launch_rows(const RowsArgs &a, hipStream_t stream) {
   const int64_t rows = (int64_t)(p.heads_q + p.heads_k) * a.S;
   const bool big_ok = a.D == 128 && !a.only_k && !a.vt && a.style != ST_FACTORED;  // where the 4-head form exists
   const int forced = thread_tuning().rows_heads;
-  const bool big_by_shape = a.style == ST_FP32 ? rows >= ROWS_BIG && a.S <= ROWS_BIG_MAX_S
-                                               : rows >= ROWS_MID_MIN && rows < ROWS_MID_END;
+  const bool big_by_shape = (rows >= ROWS_MID_MIN && rows < ROWS_MID_END) ||
+                            (a.style == ST_FP32 && rows >= ROWS_BIG && a.S <= ROWS_BIG_MAX_S);
   p.hpw = big_ok && (forced ? forced == ROWS_HPW_BIG : big_by_shape) ? ROWS_HPW_BIG : ROWS_HPW;
   const int64_t units = (p.heads_q + p.hpw - 1) / p.hpw + (p.heads_k + p.hpw - 1) / p.hpw;
   p.row_blocks = (uint32_t)(units * p.nblk);
