@@ -423,10 +423,13 @@ int pp_heads_for(int64_t Hq, int64_t Hkv) {
 // below 16 query blocks of 128 rows its per-item Q prologues and few items
 // per CU lose to the general kernel (two 4-wave workgroups per CU): B=1
 // S=1024 27 vs 33 us, B=8 S=1024 causal 100 vs 99 us (FP32 style) and 109
-// vs 105 us (HF style), B=16 S=1024 a tie.  The exception is a causal grid
+// vs 105 us (HF style), B=16 S=1024 within 2% either way by style.  The exception is a causal grid
 // whose persistent pairs give every CU exactly one (long, short) unit: B=4
-// S=1000 runs 52.4-53.1 vs 54.2-54.8 us in the FP32 style (paired ratio
-// 1.03-1.04, CI above 1) and ties at 56.5-56.8 us in the HF style.  From 16 blocks on
+// S=1000 runs 51.4-53.1 vs 53.8-54.8 us in the FP32 style (paired ratio
+// 1.03-1.04, CI above 1) and ties at 56.5-56.8 us in the HF style.  Units of
+// a few tiles do not pay for their items' prologues: B=32 S=128 (one unit
+// of 3 tiles per CU) runs 37.7 vs 35.6 us, so the exception needs 8 query
+// blocks of 128 rows.  From 16 blocks on
 // it wins when its items fill whole rounds of CUs: non-causal, when the item
 // count is a multiple of the CU count (S=2048 74.8 vs 78.4 us; S=3072, 1.5
 // rounds, 169 vs 156 us for the general kernel); causal, when the persistent
@@ -444,7 +447,7 @@ int attention_kernel_by_shape(int64_t B, int64_t Hq, int64_t Hkv, int64_t S, int
   const int64_t cus = device_cus();
   const PpGrid g = pp_grid(B, Hq, Hkv, S, causal, pp_heads_for(Hq, Hkv), cus);
   const bool paired = causal && g.persistent && thread_tuning().persistent != 1;
-  if (qb128 < 16) return paired && g.units == cus ? KFMI_KERNEL_PINGPONG : KFMI_KERNEL_GENERAL;
+  if (qb128 < 16) return paired && g.units == cus && qb128 >= 8 ? KFMI_KERNEL_PINGPONG : KFMI_KERNEL_GENERAL;
   const bool fills = causal ? paired : g.items % cus == 0;
   return fills ? KFMI_KERNEL_PINGPONG : KFMI_KERNEL_GENERAL;
 }

@@ -138,6 +138,7 @@ def test_attention_kernel_query(lib):
     assert k(8, 32, 8, 1024, 128, True, 0) == "general"     # 8 blocks, two paired units per CU
     assert k(4, 32, 8, 1000, 128, False, 0) == "general"    # 8 blocks, not causal
     assert k(1, 32, 8, 1024, 128, True, 0) == "general"     # 8 blocks, not paired
+    assert k(32, 32, 8, 128, 128, True, 0) == "general"     # one unit per CU, but of 3 tiles
     assert k(1, 32, 8, 8192, 128, True, 2) == "general"     # mode 'full'
     assert k(1, 16, 8, 8192, 256, True, 0) == "general"     # D = 256
     assert k(1, 40, 8, 8192, 128, True, 0) == "general"     # odd GQA ratio
