@@ -49,15 +49,14 @@ def test_default_hf_style_configs_3_4(gpu, b, s):
 
 
 @pytest.mark.parametrize("s", [4096, 8192])
-def test_default_hf_style_long_row_sample(gpu, s):
+def test_default_hf_style_long_whole_output(gpu, s):
     """The default 'hf' style on the ping-pong kernel (config 4 long shapes):
-    a row sample incl. first and last rows under the reference metric."""
+    the whole output under the reference metric against the FP32 oracle."""
     xs = make_inputs(1, s, QWEN3_8B, 3909)
-    announce(f"attention query hf B=1 S={s} causal")
+    announce(f"attention query hf B=1 S={s} causal (whole output)")
     out = _run(xs.to(gpu), True, norm_style="hf")
-    rows = torch.unique(torch.cat([torch.arange(0, 4), torch.arange(0, s, 97), torch.arange(s - 4, s)]))
-    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
-    m = oracle.metric(out[:, :, rows], ref)
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.metric(out, ref)
     assert m["pass"], m
 
 
@@ -99,32 +98,28 @@ def test_ragged_b4_s1000(gpu):
 
 
 @pytest.mark.parametrize("s", [4096, 8192])
-def test_long_causal_row_sample(gpu, s):
-    """Config 4 long shapes: rows sampled across the sequence, incl. first/last."""
+def test_long_causal_whole_output(gpu, s):
+    """Config 4 long shapes, every row of every head, against the FP32 oracle
+    (its SDPA run eight heads at a time to bound host memory)."""
     xs = make_inputs(1, s, QWEN3_8B, 3909)
-    announce(f"attention query fp32 B=1 S={s} causal")
+    announce(f"attention query fp32 B=1 S={s} causal (whole output)")
     out = _run(xs.to(gpu), True)
-    gen = torch.Generator().manual_seed(s)
-    rows = torch.unique(torch.cat([torch.arange(0, 4), torch.randint(0, s, (40,), generator=gen),
-                                   torch.arange(s - 4, s)]))
-    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
-    m = oracle.attention_gate(out[:, :, rows], ref)
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.attention_gate(out, ref)
     assert m["pass"], m
 
 
 @pytest.mark.parametrize("geom,b,s", [((32, 4, 128), 1, 3072), ((32, 8, 128), 3, 4096), ((8, 2, 128), 2, 3200)])
-def test_pp_geometries_row_sample(gpu, geom, b, s):
+def test_pp_geometries_whole_output(gpu, geom, b, s):
     """Ping-pong kernel shapes off the Qwen3 grid: KV heads that do not
     spread evenly over the 8 XCDs (B*Hkv = 4: heads in plain order, one item
     per workgroup; ragged S=3200), and three block pairs per CU in the
-    persistent loop (B=3, S=4096).  Two rows of every query block pass the
-    oracle gate."""
+    persistent loop (B=3, S=4096).  The whole output passes the oracle gate."""
     xs = make_inputs(b, s, geom, 5151)
-    announce(f"attention query fp32 geometry={geom} B={b} S={s} causal (ping-pong)")
+    announce(f"attention query fp32 geometry={geom} B={b} S={s} causal (ping-pong, whole output)")
     out = _run(xs.to(gpu), True)
-    rows = torch.unique(torch.cat([torch.arange(0, s, 128), torch.arange(93, s, 128), torch.tensor([s - 1])]))
-    ref = oracle.oracle_rows_fp32(*xs.astuple(), rows, True)
-    m = oracle.attention_gate(out[:, :, rows], ref)
+    ref = oracle.oracle_fp32(*xs.astuple(), True, head_chunk=8)
+    m = oracle.attention_gate(out, ref)
     assert m["pass"], m
 
 
