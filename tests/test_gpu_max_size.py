@@ -10,14 +10,16 @@ batch (the highest offsets) against the FP32 oracle on a row sample of every
 head: the fused attention prologue (ping-pong kernel, persistent, 120 units
 per CU on 256 CUs) and the isolated Q+K norm+RoPE launch.  Inputs are drawn
 on the device (seeded) to keep the host out of a 10 GB generation; the
-oracle sees the same bits through copies of the last batch.
+oracle sees the same bits through copies of the last batch.  The same
+element count at D=256 (Gemma-3-12B heads, Hq=16, Hkv=8) runs the general
+kernel, in the fused RoPE form and in the factored no-RoPE launch.
 """
 import pytest
 import torch
 
 import oracle
 from helpers import announce
-from kernelfuser_amd import QWEN3_8B, launch_attention, norm_rope
+from kernelfuser_amd import GEMMA3_12B, QWEN3_8B, launch_attention, launch_factored_attention, norm_rope
 from kernelfuser_amd.inputs import rope_tables
 
 pytestmark = pytest.mark.gpu
@@ -26,7 +28,8 @@ B, S = 15, 32768
 HQ, HKV, D = QWEN3_8B
 
 
-def _inputs(gpu):
+def _inputs(gpu, geom=QWEN3_8B):
+    HQ, HKV, D = geom
     gen = torch.Generator(device=gpu).manual_seed(31)
     rn = lambda *shape: torch.randn(*shape, generator=gen, device=gpu, dtype=torch.float32).to(torch.bfloat16)
     q = torch.empty(B, HQ, S, D, device=gpu, dtype=torch.bfloat16)
@@ -65,3 +68,30 @@ def test_max_size_attention_and_norm_rope(gpu):
         ref = oracle.rope_fp32(oracle.norm_fp32(xs, gam.cpu()), cos.cpu()[ROWS], sin.cpu()[ROWS])
         m = oracle.norm_rope_gate(got[B - 1:B, :, ROWS.to(gpu)].cpu(), ref)
         assert m["pass"], m
+
+
+def test_max_size_d256_general_and_factored(gpu):
+    hq, hkv, d = GEMMA3_12B
+    assert B * hq * S * d < 2 ** 31 and B * hq * S * d > 2 ** 31 - 2 ** 28
+    q, k, v, gq, gk, cos, sin = _inputs(gpu, GEMMA3_12B)
+    rows = ROWS.to(gpu)
+    last = [t[B - 1:B].cpu() for t in (q, k, v)]
+    announce(f"max size B={B} S={S} Gemma-3-12B: fused attention (query, fp32, causal)")
+    out = torch.empty_like(q)
+    kn = torch.empty_like(k)
+    launch_attention((q, k, v, gq, gk, cos, sin), out, causal=True, mode="query", kn=kn, norm_style="fp32")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    ref = oracle.oracle_rows_fp32(*last, gq.cpu(), gk.cpu(), cos.cpu(), sin.cpu(), ROWS, True)
+    m = oracle.attention_gate(out[B - 1:B, :, rows].cpu(), ref)
+    assert m["pass"], m
+    announce(f"max size B={B} S={S} Gemma-3-12B: factored no-RoPE attention (causal)")
+    inv = torch.empty(q.shape[:-1], device=gpu, dtype=torch.float32)
+    launch_factored_attention((q, k, v, gq, gk), out, inv, kn, causal=True)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    ref = oracle.oracle_rows_fp32(*last, gq.cpu(), gk.cpu(), None, None, ROWS, True)
+    m = oracle.attention_gate(out[B - 1:B, :, rows].cpu(), ref)
+    assert m["pass"], m
+    inv_ref = oracle.rms_inverse(last[0][:, :, ROWS].float())[..., 0]
+    assert torch.allclose(inv[B - 1:B, :, rows].cpu(), inv_ref, rtol=1e-6, atol=0)
