@@ -109,6 +109,26 @@ def test_long_causal_whole_output(gpu, s):
     assert m["pass"], m
 
 
+@pytest.mark.parametrize("s,kernel", [(2048, "attn_pp_kernel"), (3072, "attn_fwd_kernel")])
+def test_noncausal_long_whole_output(gpu, s, kernel):
+    """Non-causal prefill at B=1, whole output: S=2048 fills the CUs with
+    exactly one round of ping-pong items (256), S=3072 would need 1.5 rounds
+    and runs the general kernel (the shape-based dispatch's two sides)."""
+    from kernelfuser_amd import _lib
+    xs = make_inputs(1, s, QWEN3_8B, 4747)
+    g = xs.to(gpu)
+    out = torch.empty_like(g.q)
+    kn = torch.empty_like(g.k)
+    announce(f"attention query fp32 B=1 S={s} non-causal (whole output)")
+    recs = list(launch_attention(g.reference7, out, causal=False, mode="query", kn=kn, norm_style="fp32"))
+    torch.cuda.synchronize()
+    if _lib.attention_kernel(1, 32, 8, s, 128, False, _lib.MODE_QUERY) == ("pingpong" if kernel == "attn_pp_kernel" else "general"):
+        assert any(r["kernel"].startswith(kernel) for r in recs), recs
+    ref = oracle.oracle_fp32(*xs.astuple(), False, head_chunk=8)
+    m = oracle.attention_gate(out.cpu(), ref)
+    assert m["pass"], m
+
+
 @pytest.mark.parametrize("geom,b,s", [((32, 4, 128), 1, 3072), ((32, 8, 128), 3, 4096), ((8, 2, 128), 2, 3200)])
 def test_pp_geometries_whole_output(gpu, geom, b, s):
     """Ping-pong kernel shapes off the Qwen3 grid: KV heads that do not
