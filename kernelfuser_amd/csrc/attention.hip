@@ -39,6 +39,18 @@ __global__ __launch_bounds__(256, (D == 128 ? 2 : 1)) void attn_fwd_kernel(AttnP
   __shared__ __attribute__((aligned(1024))) unsigned char smem[4 * TILE];
 
   clock_stamp<false>(p.stamps);
+  // Two-slot pairing (slot2 > 0): the second slot holds the short causal
+  // blocks, whose workgroups have slack; they start about 12k cycles late, so
+  // the long blocks of the first slot, which set the kernel's end, stage their
+  // tables, Q rows and first tiles without that traffic.  Measured against no
+  // delay, alternated on one box: B=1 S=2048 46.5 vs 47.5 us, S=1536 33.6 vs
+  // 33.9 us, B=2 S=1024 28.1 vs 28.7 us; 6k cycles gained less at S=2048
+  // (46.8 us), 18k cycles lost at B=2 S=1024 (28.8 us).  (s_sleep n waits
+  // about 64n cycles.)
+  if (CAUSAL && p.slot2 > 0 && (int)blockIdx.x >= p.slot2) {
+    __builtin_amdgcn_s_sleep(96);
+    __builtin_amdgcn_s_sleep(96);
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
