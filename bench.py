@@ -105,11 +105,22 @@ NOMINAL_GHZ = 2.4  # MI355X peak engine clock, at which MFMA_BF16_PEAK_TFS is qu
 def clock_of(kf, fn, launches=200):
     """Shader clock during `fn`'s attention launches: `launches` back-to-back
     calls with per-workgroup clock stamps on (kfmi_clock_stamps), summarised
-    over the last launch's workgroups; results are unchanged by the stamps."""
-    with kf._lib.tuning(clock_stamps=1):
-        for _ in range(launches):
-            fn()
-    return kf._lib.clock_summary(kf._lib.clock_stamps())
+    over the last launch's workgroups; results are unchanged by the stamps.
+    None (and a note on stderr) if the stamps cannot be read: the clock is
+    reported beside the measured figures, never in place of them."""
+    try:
+        with kf._lib.tuning(clock_stamps=1):
+            for _ in range(launches):
+                fn()
+        return kf._lib.clock_summary(kf._lib.clock_stamps())
+    except (RuntimeError, ValueError) as e:
+        print(f"bench: clock stamps unavailable: {e}", file=sys.stderr, flush=True)
+        return None
+
+
+def at_clock(tflops, clock):
+    """Fraction of the MFMA peak scaled to the measured clock (None without one)."""
+    return None if clock is None else tflops / (MFMA_BF16_PEAK_TFS * clock["ghz_median"] / NOMINAL_GHZ)
 
 
 def headline(args, torch, kf):
@@ -233,11 +244,11 @@ def prefill_shapes(args, torch, kf):
                                            norm_style=args.norm_style)
         ms = time_graph(lambda i: step(), 20)
         f = kf.attention_flops(b, hq, s, d, True)
-        ghz = clock_of(kf, step)["ghz_median"]
+        clk = clock_of(kf, step)
+        tf = f / (ms * 1e-3) / 1e12
         rows.append({"B": b, "S": s, "kernel": kf._lib.attention_kernel(b, hq, hkv, s, d, True, kf._lib.MODE_QUERY),
-                     "us": ms * 1e3, "tflops": f / (ms * 1e-3) / 1e12,
-                     "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS, "clock_ghz": ghz,
-                     "frac_mfma_at_clock": f / (ms * 1e-3) / 1e12 / (MFMA_BF16_PEAK_TFS * ghz / NOMINAL_GHZ)})
+                     "us": ms * 1e3, "tflops": tf, "frac_mfma": tf / MFMA_BF16_PEAK_TFS,
+                     "clock_ghz": None if clk is None else clk["ghz_median"], "frac_mfma_at_clock": at_clock(tf, clk)})
         del xs, out, kn
     return rows
 
@@ -252,10 +263,11 @@ def factored(args, torch, kf):
                                                 bn=64)
     ms = time_graph(lambda i: step(), 20)
     f = kf.attention_flops(b, hq, s, d, True)
-    ghz = clock_of(kf, step)["ghz_median"]
+    clk = clock_of(kf, step)
+    tf = f / (ms * 1e-3) / 1e12
     return {"B": b, "S": s, "Hq": hq, "Hkv": hkv, "D": d, "causal": True, "us": ms * 1e3,
-            "tflops": f / (ms * 1e-3) / 1e12, "frac_mfma": f / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFS,
-            "clock_ghz": ghz, "frac_mfma_at_clock": f / (ms * 1e-3) / 1e12 / (MFMA_BF16_PEAK_TFS * ghz / NOMINAL_GHZ)}
+            "tflops": tf, "frac_mfma": tf / MFMA_BF16_PEAK_TFS,
+            "clock_ghz": None if clk is None else clk["ghz_median"], "frac_mfma_at_clock": at_clock(tf, clk)}
 
 
 def cpu_baseline(args, torch, xs_cpu, out_gpu):
@@ -398,13 +410,13 @@ def main():
                      "frac_note": "frac: attention kernel alone (graph-replay events); frac_step_*: the whole "
                                   "step (K-prep launch + attention, K steps replayed as one HIP graph) by "
                                   "device events / by the host clock",
-                     "clock": dict(head["clock"], nominal_ghz=NOMINAL_GHZ,
-                                   peak_at_clock=MFMA_BF16_PEAK_TFS * head["clock"]["ghz_median"] / NOMINAL_GHZ,
-                                   frac_at_clock=head["attention_kernel_tflops"]
-                                   / (MFMA_BF16_PEAK_TFS * head["clock"]["ghz_median"] / NOMINAL_GHZ),
-                                   note="shader clock of the attention kernel's workgroups (per-workgroup "
-                                        "s_memtime / s_memrealtime stamps, 200 back-to-back launches, last "
-                                        "launch); peak_at_clock scales the 2.5 PFLOP/s peak to that clock")},
+                     "clock": None if head["clock"] is None else dict(
+                         head["clock"], nominal_ghz=NOMINAL_GHZ,
+                         peak_at_clock=MFMA_BF16_PEAK_TFS * head["clock"]["ghz_median"] / NOMINAL_GHZ,
+                         frac_at_clock=at_clock(head["attention_kernel_tflops"], head["clock"]),
+                         note="shader clock of the attention kernel's workgroups (per-workgroup "
+                              "s_memtime / s_memrealtime stamps, 200 back-to-back launches, last "
+                              "launch); peak_at_clock scales the 2.5 PFLOP/s peak to that clock")},
         "kernels": {"attention_us": head["attention_kernel_us"],
                     "prep_us": head["prep_kernel_us"], "prep_bytes": head["prep_bytes"],
                     "prep_gbs": head["prep_gbs"], "prep": "K RMSNorm+RoPE rows (one launch)",
