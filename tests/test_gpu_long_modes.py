@@ -8,7 +8,9 @@ src/e1_qk_publication_v3.py:612-638):
   * mode 'unfused' at S=8192: Q and K prepared by one launch, then the
     ping-pong kernel without a prologue;
   * the factored no-RoPE launch at S=4096 with D=128 (ping-pong kernel, Q's
-    inverse RMS computed in its prologue) and D=256 (general kernel).
+    inverse RMS computed in its prologue) and D=256 (general kernel);
+  * query mode with Gemma-3-12B heads (D=256) at S=4096 and Qwen3-32B heads
+    at S=2048.
 """
 import pytest
 import torch
@@ -53,3 +55,23 @@ def test_long_factored_whole_output(gpu, geom):
     assert m["pass"], m
     inv_ref = oracle.rms_inverse(xs.q.float())[..., 0]
     assert torch.allclose(inv.cpu(), inv_ref, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("geom,s,causal,style", [(GEMMA3_12B, 4096, True, "fp32"), (GEMMA3_12B, 4096, False, "legacy"),
+                                                 ((64, 8, 128), 2048, True, "fp32")])
+def test_long_query_geometries_whole_output(gpu, geom, s, causal, style):
+    """Query mode at long S off the Qwen3-8B geometry: Gemma-3-12B heads (D=256,
+    general kernel, RoPE in the prologue), causal and not, and Qwen3-32B heads
+    (GQA ratio 8: two four-head items per KV head; the persistent pairing fills
+    every CU at S=2048)."""
+    xs = make_inputs(1, s, geom, 8282)
+    g = xs.to(gpu)
+    out = torch.full_like(g.q, float("nan"))
+    kn = torch.empty_like(g.k)
+    announce(f"long query {geom} {style} B=1 S={s} causal={causal} (whole output)")
+    launch_attention(g.reference7, out, causal=causal, mode="query", kn=kn, norm_style=style)
+    torch.cuda.synchronize()
+    ref = oracle.oracle_fp32(*xs.astuple(), causal, head_chunk=8)
+    gate = oracle.attention_gate if style == "fp32" else oracle.metric
+    m = gate(out.cpu(), ref)
+    assert m["pass"], m
