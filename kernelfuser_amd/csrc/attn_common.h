@@ -850,11 +850,18 @@ __device__ __forceinline__ void store_rows_lds(unsigned char *tile, uint16_t *ob
   }
 }
 
+// The bits of x as an integer the compiler cannot trace back to a float.  In
+// files built without NaN semantics a test of the exponent bits of a value
+// that comes from floating-point arithmetic is otherwise rewritten as a
+// floating-point class test (fabs(x) == inf, unordered) whose operand is
+// assumed not NaN, and a NaN then passes it.
+__device__ __forceinline__ uint32_t opaque_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  asm("" : "+v"(u));
+  return u;
+}
 __device__ __forceinline__ bool not_finite(float x) {
-  // exponent field all ones (inf or NaN), tested on the bits so that no
-  // floating-point assumption of the build can fold it away (for a value
-  // that cannot be NaN, such as a sum of non-negative numbers)
-  return (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u;
+  return (opaque_bits(x) & 0x7f800000u) == 0x7f800000u;  // exponent field all ones: inf or NaN
 }
 // Any accumulator inf or NaN: the largest magnitude bit pattern is at least
 // the exponent-all-ones pattern.  Integer arithmetic on one accumulator
@@ -868,7 +875,7 @@ __device__ __forceinline__ bool any_not_finite(const f32x16_t (&o)[N]) {
   for (int n = 0; n < N; ++n)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t a = __float_as_uint(o[n][i]) & 0x7fffffffu;
+      const uint32_t a = opaque_bits(o[n][i]) & 0x7fffffffu;
       m[i & 1] = m[i & 1] > a ? m[i & 1] : a;
     }
   return (m[0] > m[1] ? m[0] : m[1]) >= 0x7f800000u;

@@ -1,0 +1,83 @@
+"""Seeded sweep over the prologue's configuration space, each case checked on
+its whole output against the CPU FP32 oracle (src/e1_rope_publication_v1.py:
+295-302; no-RoPE factored: :736-742 and src/e1_qk_publication_v3.py:612-638).
+
+The other GPU tests vary one or two settings around fixed shapes.  Here 40
+cases drawn from a fixed seed mix them: a geometry of the reference's MODELS
+table (rope:31-36), B in 1..3, S from a list dense in tile and block edges
+(1 to 700), causal or not, the launcher path ('query', 'unfused', 'full' or
+the factored launch), the rounding style, RoPE on or off, and the attention
+kernel (by shape, or forced to each kernel the geometry admits).  The case
+list depends only on the seed, so every run checks the same cases.  Each test
+names its case before the GPU step and checks from the launch records that a
+forced kernel ran.
+"""
+import random
+
+import pytest
+import torch
+
+import oracle
+from helpers import announce
+from kernelfuser_amd import MODELS, _lib, launch_attention, launch_factored_attention, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+S_CHOICES = [1, 2, 7, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 191, 200, 255, 256, 257, 300, 383, 448,
+             511, 513, 640, 700]
+KERNEL_PREFIX = {"general": "attn_fwd_kernel", "pingpong": "attn_pp_kernel", "wide": "attn_ww_kernel"}
+
+
+def _cases(n=40, seed=4242):
+    rng = random.Random(seed)
+    geoms = sorted(MODELS.items())
+    cases = []
+    for i in range(n):
+        name, (hq, hkv, d) = rng.choice(geoms)
+        b = rng.choice([1, 1, 2, 3])
+        s = rng.choice(S_CHOICES)
+        causal = rng.random() < 0.5
+        path = rng.choice(["query", "query", "unfused", "full", "factored"])
+        rope = path != "factored" and rng.random() < 0.75
+        style = "factored" if path == "factored" else rng.choice(["fp32", "hf", "legacy"])
+        kernels = ["auto", "general"]
+        if path != "full" and d == 128 and (hq // hkv) % 2 == 0:
+            kernels.append("pingpong")
+        if path != "full" and d == 128 and (hq // hkv) % 4 == 0:
+            kernels.append("wide")
+        kernel = rng.choice(kernels)
+        cid = f"{i:02d}-{name}-B{b}-S{s}-{'c' if causal else 'nc'}-{path}-{style}-{'rope' if rope else 'norope'}-{kernel}"
+        cases.append(pytest.param(name, b, s, causal, path, style, rope, kernel, id=cid))
+    return cases
+
+
+@pytest.mark.parametrize("name,b,s,causal,path,style,rope,kernel", _cases())
+def test_sweep_case_whole_output(gpu, name, b, s, causal, path, style, rope, kernel):
+    geom = MODELS[name]
+    xs = make_inputs(b, s, geom, 5000 + 7 * s + b, rope=rope)
+    g = xs.to(gpu)
+    out = torch.full_like(g.q, float("nan"))
+    kn = torch.empty_like(g.k)
+    announce(f"sweep {name} {geom} B={b} S={s} causal={causal} {path} {style} rope={rope} kernel={kernel}")
+    with _lib.tuning(attn_kernel=kernel):
+        if path == "factored":
+            inv = torch.empty(g.q.shape[:-1], device=gpu, dtype=torch.float32)
+            recs = list(launch_factored_attention((g.q, g.k, g.v, g.gq, g.gk), out, inv, kn, causal=causal))
+        else:
+            qn = torch.empty_like(g.q) if path == "unfused" else None
+            recs = list(launch_attention(g.reference7, out, causal=causal, mode=path, rope=rope, qn=qn, kn=kn,
+                                         norm_style=style))
+    torch.cuda.synchronize()
+    attn = [r["kernel"] for r in recs if r["kernel"].startswith("attn_")]
+    assert len(attn) == 1, recs
+    if kernel != "auto":
+        assert attn[0].startswith(KERNEL_PREFIX[kernel]), attn
+    if path == "factored":
+        ref = oracle.refinement_oracle_norope(xs.q, xs.k, xs.v, xs.gq, xs.gk, causal)
+        inv_ref = oracle.rms_inverse(xs.q.float())[..., 0]
+        assert torch.allclose(inv.cpu(), inv_ref, rtol=1e-6, atol=0)
+    else:
+        ref = oracle.oracle_fp32(*xs.astuple(), causal)
+    gate = oracle.metric if style in ("hf", "legacy") else oracle.attention_gate
+    m = gate(out.cpu(), ref)
+    assert m["pass"], m

@@ -9,8 +9,9 @@ Cases: ragged and tiny S (one key tile, a partial tile, tails past a 64-row
 block), both causal modes, the FOLD (fp32) and scaled (hf, legacy,
 prepared-Q, factored) softmax paths, GQA ratios 4 and 8, head counts that do
 not spread over the 8 XCDs, the persistent long/short pairing (B=4, S=1000:
-256 pairs), tensors followed by NaN (no read past S), and inputs built to
-overflow the lean softmax (a spiked key; huge V) so that the exact redo runs.
+256 pairs), tensors followed by NaN (no read past S), inputs built to
+overflow the lean softmax (a spiked key; huge V) so that the exact redo runs,
+and one-tile items after a launch that left NaN bits in LDS.
 """
 import pytest
 import torch
@@ -154,6 +155,40 @@ def test_wide_ragged_tiles_read_zeros(gpu, b, s):
                                    torch.arange(max(0, s - 4), s)]))
     m = oracle.attention_gate(out[:, :, rows.to(gpu)].cpu(), oracle.oracle_rows_fp32(*xs.astuple(), rows, True))
     assert m["pass"], m
+
+
+@pytest.mark.parametrize("geom,b,s,causal,mode,style,tun", [
+    ((64, 8, 128), 3, 64, False, "unfused", "legacy", {}),
+    ((64, 8, 128), 1, 32, False, "unfused", "legacy", {}),
+    ((64, 8, 128), 3, 64, True, "query", "hf", {}),
+    (QWEN3_8B, 3, 64, False, "query", "fp32", {}),
+    (QWEN3_8B, 2, 300, True, "query", "fp32", {"persistent": 1}),
+])
+def test_wide_one_tile_items_after_nan_in_lds(gpu, geom, b, s, causal, mode, style, tun):
+    """Items of one key tile after a launch that left NaN bits in LDS.  The
+    wide kernel's last iteration multiplies its second K buffer (scores that
+    must give probabilities of 0), and LDS keeps what earlier workgroups
+    wrote: a wide launch on an all-NaN Q first stages NaN output rows through
+    that region.  Such an item used to return NaN rows: its dead GEMM1 read
+    the stale NaN bits, and the NaN row sum passed the redo check, which the
+    compiler had rewritten as a class test assuming no NaN.  Cases: S <= 64
+    (one tile per item), and causal S=300 with one item per workgroup (block
+    0 holds one tile; its second buffer now gets the real keys 64..127).
+    Three rounds each."""
+    dirty = make_inputs(3, 700, (64, 8, 128), 8787).to(gpu)
+    dirty.q.fill_(float("nan"))
+    xs = make_inputs(b, s, geom, 8888 + s + b)
+    g = xs.to(gpu)
+    ref = oracle.oracle_fp32(*xs.astuple(), causal)
+    gate = oracle.attention_gate if style == "fp32" else oracle.metric
+    announce(f"wide one-tile items after NaN in LDS {geom} B={b} S={s} causal={causal} {mode} {style} {tun}")
+    for _ in range(3):
+        dirty_out, _ = _launch(dirty, False, mode="unfused", norm_style="legacy")
+        assert not bool(torch.isfinite(dirty_out.float()).any())
+        out, recs = _launch(g, causal, mode=mode, norm_style=style, **tun)
+        _ran_wide(recs)
+        m = gate(out, ref)
+        assert m["pass"], m
 
 
 def _spiked(s, key, k0, vscale, seed):
