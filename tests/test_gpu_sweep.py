@@ -2,15 +2,17 @@
 its whole output against the CPU FP32 oracle (src/e1_rope_publication_v1.py:
 295-302; no-RoPE factored: :736-742 and src/e1_qk_publication_v3.py:612-638).
 
-The other GPU tests vary one or two settings around fixed shapes.  Here 40
+The other GPU tests vary one or two settings around fixed shapes.  Here
 cases drawn from a fixed seed mix them: a geometry of the reference's MODELS
-table (rope:31-36), B in 1..3, S from a list dense in tile and block edges
-(1 to 700), causal or not, the launcher path ('query', 'unfused', 'full' or
-the factored launch), the rounding style, RoPE on or off, and the attention
-kernel (by shape, or forced to each kernel the geometry admits).  The case
-list depends only on the seed, so every run checks the same cases.  Each test
-names its case before the GPU step and checks from the launch records that a
-forced kernel ran.
+table (rope:31-36), B, S from a list dense in tile and block edges, causal or
+not, the launcher path ('query', 'unfused', 'full' or the factored launch),
+the rounding style, RoPE on or off, and the attention kernel (by shape, or
+forced to each kernel the geometry admits).  Two draws: 40 short cases (B in
+1..3, S from 1 to 700: one-tile items, partial tiles) and 30 long ones (B in
+1..2, S from 777 to 4096: the dispatch thresholds, the persistent pairing, the
+D=256 split plans).  The case lists depend only on the seeds, so every run
+checks the same cases.  Each test names its case before the GPU step and
+checks from the launch records that a forced kernel ran.
 """
 import random
 
@@ -25,17 +27,18 @@ pytestmark = pytest.mark.gpu
 
 S_CHOICES = [1, 2, 7, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 191, 200, 255, 256, 257, 300, 383, 448,
              511, 513, 640, 700]
+S_LONG = [777, 1000, 1023, 1024, 1025, 1500, 1536, 1900, 2047, 2048, 2049, 2945, 3000, 3072, 4095, 4096]
 KERNEL_PREFIX = {"general": "attn_fwd_kernel", "pingpong": "attn_pp_kernel", "wide": "attn_ww_kernel"}
 
 
-def _cases(n=40, seed=4242):
+def _cases(n, seed, s_choices=S_CHOICES, b_choices=(1, 1, 2, 3)):
     rng = random.Random(seed)
     geoms = sorted(MODELS.items())
     cases = []
     for i in range(n):
         name, (hq, hkv, d) = rng.choice(geoms)
-        b = rng.choice([1, 1, 2, 3])
-        s = rng.choice(S_CHOICES)
+        b = rng.choice(b_choices)
+        s = rng.choice(s_choices)
         causal = rng.random() < 0.5
         path = rng.choice(["query", "query", "unfused", "full", "factored"])
         rope = path != "factored" and rng.random() < 0.75
@@ -51,8 +54,17 @@ def _cases(n=40, seed=4242):
     return cases
 
 
-@pytest.mark.parametrize("name,b,s,causal,path,style,rope,kernel", _cases())
+@pytest.mark.parametrize("name,b,s,causal,path,style,rope,kernel", _cases(40, 4242))
 def test_sweep_case_whole_output(gpu, name, b, s, causal, path, style, rope, kernel):
+    _check_case(gpu, name, b, s, causal, path, style, rope, kernel)
+
+
+@pytest.mark.parametrize("name,b,s,causal,path,style,rope,kernel", _cases(30, 9001, S_LONG, (1, 1, 2)))
+def test_sweep_long_case_whole_output(gpu, name, b, s, causal, path, style, rope, kernel):
+    _check_case(gpu, name, b, s, causal, path, style, rope, kernel)
+
+
+def _check_case(gpu, name, b, s, causal, path, style, rope, kernel):
     geom = MODELS[name]
     xs = make_inputs(b, s, geom, 5000 + 7 * s + b, rope=rope)
     g = xs.to(gpu)
@@ -73,11 +85,11 @@ def test_sweep_case_whole_output(gpu, name, b, s, causal, path, style, rope, ker
     if kernel != "auto":
         assert attn[0].startswith(KERNEL_PREFIX[kernel]), attn
     if path == "factored":
-        ref = oracle.refinement_oracle_norope(xs.q, xs.k, xs.v, xs.gq, xs.gk, causal)
+        ref = oracle.refinement_oracle_norope(xs.q, xs.k, xs.v, xs.gq, xs.gk, causal, head_chunk=8)
         inv_ref = oracle.rms_inverse(xs.q.float())[..., 0]
         assert torch.allclose(inv.cpu(), inv_ref, rtol=1e-6, atol=0)
     else:
-        ref = oracle.oracle_fp32(*xs.astuple(), causal)
+        ref = oracle.oracle_fp32(*xs.astuple(), causal, head_chunk=8)
     gate = oracle.metric if style in ("hf", "legacy") else oracle.attention_gate
     m = gate(out.cpu(), ref)
     assert m["pass"], m
