@@ -875,7 +875,7 @@ __device__ __forceinline__ bool any_not_finite(const f32x16_t (&o)[N]) {
   for (int n = 0; n < N; ++n)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const uint32_t a = opaque_bits(o[n][i]) & 0x7fffffffu;
+      const uint32_t a = __float_as_uint(o[n][i]) & 0x7fffffffu;
       m[i & 1] = m[i & 1] > a ? m[i & 1] : a;
     }
   return (m[0] > m[1] ? m[0] : m[1]) >= 0x7f800000u;

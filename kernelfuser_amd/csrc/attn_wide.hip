@@ -304,11 +304,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       copy16_to_lds(srs, lds0 + TAB + TAB_BYTES + j * 1024, voff);
     }
   }
-  // K(1) also when the item has one tile: the last iteration's GEMM1 reads
-  // this buffer, and LDS keeps whatever earlier workgroups left there (NaN
-  // or inf bits make its -inf start NaN).  Past the head's last key the copy
-  // reads zeros (range check); a causal block 0 gets the real keys 64..127.
-  copy_k(1, K1);
+  if (nT > 1) copy_k(1, K1);
   copy_v(0, V0);
 
   bf16x8_t qreg[2][NC];
@@ -466,9 +462,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // its first step is masked before the previous iteration computes it (that
   // key block is complete by round 2), the rest at the start of its own
   // iteration.  The last iteration has no tile t+1: its GEMM1 starts from
-  // -inf, so the scores it makes (of the finite K rows the buffer holds: a
-  // copied tile or zeros) give probabilities of exactly 0 and add nothing to
-  // the row sums.
+  // -inf, so the scores it makes of finite K rows give probabilities of
+  // exactly 0 and add nothing to the row sums.  An item of one tile never
+  // fills that buffer, and LDS keeps whatever earlier workgroups left there:
+  // NaN or inf bits make NaN row sums, which send the item to the exact redo
+  // (not_finite tests the bits through an empty asm, so no build assumption
+  // removes that check).  Copying a tile into the buffer for such items
+  // instead made the compiler spill more registers (S=2048 non-causal, HF
+  // style: 5% slower).
   auto iter = [&](auto par, int t, f32x16_t (&cur)[2][2], f32x16_t (&nxt)[2][2]) {
     constexpr int PAR = decltype(par)::value;
     constexpr int KN = PAR ? K0 : K1, VC = PAR ? V1 : V0, KO = PAR ? K1 : K0;

@@ -167,14 +167,14 @@ def test_wide_ragged_tiles_read_zeros(gpu, b, s):
 def test_wide_one_tile_items_after_nan_in_lds(gpu, geom, b, s, causal, mode, style, tun):
     """Items of one key tile after a launch that left NaN bits in LDS.  The
     wide kernel's last iteration multiplies its second K buffer (scores that
-    must give probabilities of 0), and LDS keeps what earlier workgroups
-    wrote: a wide launch on an all-NaN Q first stages NaN output rows through
-    that region.  Such an item used to return NaN rows: its dead GEMM1 read
-    the stale NaN bits, and the NaN row sum passed the redo check, which the
-    compiler had rewritten as a class test assuming no NaN.  Cases: S <= 64
-    (one tile per item), and causal S=300 with one item per workgroup (block
-    0 holds one tile; its second buffer now gets the real keys 64..127).
-    Three rounds each."""
+    must give probabilities of 0), which an item of one tile never fills, and
+    LDS keeps what earlier workgroups wrote: a wide launch on an all-NaN Q
+    first stages NaN output rows through that region.  The NaN row sums must
+    send such items to the exact redo; they used to pass the redo check,
+    which the compiler had rewritten as a class test assuming no NaN, and the
+    items returned NaN rows.  Cases: S <= 64 (one tile per item), and causal
+    S=300 with one item per workgroup (block 0 holds one tile).  Three rounds
+    each."""
     dirty = make_inputs(3, 700, (64, 8, 128), 8787).to(gpu)
     dirty.q.fill_(float("nan"))
     xs = make_inputs(b, s, geom, 8888 + s + b)
