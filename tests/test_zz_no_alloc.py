@@ -140,3 +140,23 @@ def test_noalloc_oversized_plan_runs_unsplit(gpu):
     assert p1 == p2 and p1[0].startswith("split=0"), (p1, p2)
     assert bool(torch.isfinite(o1).all())
     assert torch.equal(o1, o2) and torch.equal(k1, k2)
+
+
+def test_noalloc_seeded_sequence_of_split_plans(gpu):
+    """Twelve D=256 shapes drawn from a fixed seed (Gemma-3-4B and -12B heads,
+    B in 1..2, S in 65..2100, mostly causal) run back to back: split plans of
+    6-33 MiB in varying order of size, with unsplit shapes between them, so
+    each call finds the array as a different plan left it.  Every call equals
+    the workspace entry point bit for bit."""
+    import random
+
+    rng = random.Random(3131)
+    for i in range(12):
+        geom = rng.choice([(8, 4, 256), (16, 8, 256)])
+        b = rng.choice([1, 1, 2])
+        s = rng.randint(65, 2100)
+        causal = rng.random() < 0.75
+        assert attention_workspace_bytes(b, geom[0], geom[1], s, geom[2], causal) <= 36 << 20
+        xs = make_inputs(b, s, geom, 3200 + i).to(gpu)
+        announce(f"noalloc sequence {i}: {geom} B={b} S={s} causal={causal}")
+        _compare(xs, causal, MODE_QUERY)
