@@ -7,11 +7,12 @@ cases drawn from a fixed seed mix them: a geometry of the reference's MODELS
 table (rope:31-36), B, S from a list dense in tile and block edges, causal or
 not, the launcher path ('query', 'unfused', 'full' or the factored launch),
 the rounding style, RoPE on or off, and the attention kernel (by shape, or
-forced to each kernel the geometry admits).  Two draws: 40 short cases (B in
+forced to each kernel the geometry admits).  Draws: 40 short cases (B in
 1..3, S from 1 to 700: one-tile items, partial tiles) and 30 long ones (B in
 1..2, S from 777 to 4096: the dispatch thresholds, the persistent pairing, the
-D=256 split plans).  The case lists depend only on the seeds, so every run
-checks the same cases.  Each test names its case before the GPU step and
+D=256 split plans), plus 20 short cases on geometries beyond the reference's
+table (MHA and odd GQA ratios, general kernel only).  The case lists depend
+only on the seeds, so every run checks the same cases.  Each test names its case before the GPU step and
 checks from the launch records that a forced kernel ran.
 """
 import random
@@ -28,12 +29,18 @@ pytestmark = pytest.mark.gpu
 S_CHOICES = [1, 2, 7, 31, 32, 33, 63, 64, 65, 96, 127, 128, 129, 191, 200, 255, 256, 257, 300, 383, 448,
              511, 513, 640, 700]
 S_LONG = [777, 1000, 1023, 1024, 1025, 1500, 1536, 1900, 2047, 2048, 2049, 2945, 3000, 3072, 4095, 4096]
+# geometries the boundary accepts beyond the reference's table: MHA (ratio 1)
+# and odd GQA ratios, which only the general kernel serves
+OFF_TABLE = {"MHA-8x128": (8, 8, 128), "MHA-5x128": (5, 5, 128), "MHA-4x256": (4, 4, 256),
+             "GQA3-12q4kv-128": (12, 4, 128), "GQA3-24q8kv-128": (24, 8, 128), "GQA5-40q8kv-128": (40, 8, 128),
+             "GQA3-6q2kv-256": (6, 2, 256), "GQA2-10q5kv-256": (10, 5, 256)}
+GEOMETRIES = {**MODELS, **OFF_TABLE}
 KERNEL_PREFIX = {"general": "attn_fwd_kernel", "pingpong": "attn_pp_kernel", "wide": "attn_ww_kernel"}
 
 
-def _cases(n, seed, s_choices=S_CHOICES, b_choices=(1, 1, 2, 3)):
+def _cases(n, seed, s_choices=S_CHOICES, b_choices=(1, 1, 2, 3), table=MODELS):
     rng = random.Random(seed)
-    geoms = sorted(MODELS.items())
+    geoms = sorted(table.items())
     cases = []
     for i in range(n):
         name, (hq, hkv, d) = rng.choice(geoms)
@@ -64,8 +71,13 @@ def test_sweep_long_case_whole_output(gpu, name, b, s, causal, path, style, rope
     _check_case(gpu, name, b, s, causal, path, style, rope, kernel)
 
 
+@pytest.mark.parametrize("name,b,s,causal,path,style,rope,kernel", _cases(20, 5151, table=OFF_TABLE))
+def test_sweep_off_table_case_whole_output(gpu, name, b, s, causal, path, style, rope, kernel):
+    _check_case(gpu, name, b, s, causal, path, style, rope, kernel)
+
+
 def _check_case(gpu, name, b, s, causal, path, style, rope, kernel):
-    geom = MODELS[name]
+    geom = GEOMETRIES[name]
     xs = make_inputs(b, s, geom, 5000 + 7 * s + b, rope=rope)
     g = xs.to(gpu)
     out = torch.full_like(g.q, float("nan"))
