@@ -68,7 +68,9 @@ def main(argv: list[str]) -> int:
     out = Path(argv[0]) if argv else Path(tempfile.mkdtemp(prefix="kfmi-asan-"))
     lib = build_sanitized(out)
     (out / "kfmi_asan_plugin.py").write_text(PLUGIN.format(lib=str(lib)))
-    env = {"LD_PRELOAD": asan_runtime(), "ASAN_OPTIONS": "detect_leaks=0:verify_asan_link_order=0:halt_on_error=1",
+    # the ASAN runtime first; whatever the environment already preloads stays
+    preload = " ".join(p for p in (asan_runtime(), os.environ.get("LD_PRELOAD", "")) if p)
+    env = {"LD_PRELOAD": preload, "ASAN_OPTIONS": "detect_leaks=0:verify_asan_link_order=0:halt_on_error=1",
            "UBSAN_OPTIONS": "print_stacktrace=1:halt_on_error=1", "PYTHONPATH": str(out)}
     cmd = [sys.executable, "-m", "pytest", "-p", "kfmi_asan_plugin", str(ROOT / "tests"), "-q", "-m", "not gpu",
            "--deselect", "tests/test_c_caller.py", "--deselect", "tests/test_nan_checks_ir.py"]
