@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define KFMI_ABI_VERSION 9
+#define KFMI_ABI_VERSION 10
 
 /* status codes */
 #define KFMI_OK 0
@@ -256,20 +256,26 @@ int kfmi_factored_prepare_bf16(const void *q, const void *k, const void *gq, con
  * with exp2 online softmax; q is the RAW (un-normalised) BF16 query.
  * inv_mode = 0: read inv (written by kfmi_factored_prepare_bf16);
  * inv_mode = 1: compute each row's inverse RMS from q in the prologue
- * (eps) and also write it to inv (which may then be NULL to skip the write). */
+ * (eps) and also write it to inv (which may then be NULL to skip the write).
+ * work / work_bytes: the optional split-KV workspace, as for
+ * kfmi_launch_attention_bf16 (same plan, same kfmi_attention_workspace_bytes;
+ * NULL runs unsplit). */
 int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, float *inv,
                                  void *out, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
                                  int64_t D, float eps, int causal, int inv_mode, int bm, int bn,
-                                 void *stream);
+                                 void *work, int64_t work_bytes, void *stream);
 
 /* Both launches of launch_factored_attention (qk:641-652): KN preparation
  * for the K rows, then factored attention that computes INV in its prologue
- * and writes it to inv.  Outputs out, inv and kn match the reference's. */
+ * and writes it to inv.  Outputs out, inv and kn match the reference's.
+ * work / work_bytes: the optional split-KV workspace of the attention launch
+ * (as for kfmi_launch_attention_bf16; NULL runs unsplit).  The reference's
+ * launcher takes none. */
 int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void *v,
                                         const void *gq, const void *gk, void *out, float *inv,
                                         void *kn, int64_t B, int64_t Hq, int64_t Hkv, int64_t S,
                                         int64_t D, float eps, int causal, int bm, int bn,
-                                        void *stream);
+                                        void *work, int64_t work_bytes, void *stream);
 
 #ifdef __cplusplus
 }

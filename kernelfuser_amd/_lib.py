@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkfmi.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 KFMI_OK, KFMI_EINVAL, KFMI_ELAUNCH, KFMI_EDEVICE = 0, 1, 2, 3
 NORM_STYLES = {"hf": 0, "legacy": 1, "fp32": 2}
@@ -42,9 +42,10 @@ SIGNATURES = {
     "kfmi_launch_attention_bf16_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
                                            _D, _F, _I, _I, _I, _I, _I, _P],
     "kfmi_factored_prepare_bf16": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
-    "kfmi_factored_attention_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P],
+    "kfmi_factored_attention_bf16": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I, _I, _I, _I, _P,
+                                     _I64, _P],
     "kfmi_launch_factored_attention_bf16": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F, _I,
-                                            _I, _I, _P],
+                                            _I, _I, _P, _I64, _P],
 }
 
 _lock = threading.Lock()

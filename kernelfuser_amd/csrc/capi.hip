@@ -411,9 +411,10 @@ int kfmi_factored_prepare_bf16(const void *q, const void *k, const void *gq, con
 
 int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, float *inv, void *out, int64_t B,
                                  int64_t Hq, int64_t Hkv, int64_t S, int64_t D, float eps, int causal, int inv_mode,
-                                 int bm, int bn, void *stream) {
+                                 int bm, int bn, void *work, int64_t work_bytes, void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_tiles(bm, bn));
+  KFMI_TRY(check_work(work, work_bytes));
   KFMI_TRY(check_ptrs({{q, "q"}, {kn, "kn"}, {v, "v"}, {out, "out"}}));
   if (inv_mode != 0 && inv_mode != 1) return fail(KFMI_EINVAL, "inv_mode must be 0 (read) or 1 (compute)");
   if (inv_mode == 0) KFMI_TRY(check_ptrs({{inv, "inv"}}));
@@ -422,14 +423,16 @@ int kfmi_factored_attention_bf16(const void *q, const void *kn, const void *v, f
   KFMI_TRY(check_device());
   const int pro = inv_mode == 0 ? kfmi::PRO_FACTORED_READ : kfmi::PRO_FACTORED_CALC;
   return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal, pro,
-                        kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
+                        kfmi::ST_FP32, bm, bn, (hipStream_t)stream, work, work_bytes);
 }
 
 int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void *v, const void *gq, const void *gk,
                                         void *out, float *inv, void *kn, int64_t B, int64_t Hq, int64_t Hkv,
-                                        int64_t S, int64_t D, float eps, int causal, int bm, int bn, void *stream) {
+                                        int64_t S, int64_t D, float eps, int causal, int bm, int bn, void *work,
+                                        int64_t work_bytes, void *stream) {
   KFMI_TRY(check_shape(B, Hq, Hkv, S, D));
   KFMI_TRY(check_tiles(bm, bn));
+  KFMI_TRY(check_work(work, work_bytes));
   KFMI_TRY(check_ptrs({{q, "q"}, {k, "k"}, {v, "v"}, {gq, "gq"}, {gk, "gk"}, {out, "out"}, {inv, "inv"}, {kn, "kn"}}));
   if (!(eps >= 0.0f)) return fail(KFMI_EINVAL, "eps must be >= 0");
   KFMI_TRY(check_tuning(Hq, Hkv, D, false));
@@ -442,7 +445,7 @@ int kfmi_launch_factored_attention_bf16(const void *q, const void *k, const void
   hipError_t e = kfmi::launch_rows(r, (hipStream_t)stream);
   if (e != hipSuccess) return launch_status(e, "factored prepare launch");
   return attention_impl(q, kn, v, nullptr, nullptr, nullptr, nullptr, nullptr, out, inv, B, Hq, Hkv, S, D, 0.0, eps, causal,
-                        kfmi::PRO_FACTORED_CALC, kfmi::ST_FP32, bm, bn, (hipStream_t)stream);
+                        kfmi::PRO_FACTORED_CALC, kfmi::ST_FP32, bm, bn, (hipStream_t)stream, work, work_bytes);
 }
 
 }  // extern "C"

@@ -234,19 +234,21 @@ def transpose_v(v, vt):
     _lib.call("kfmi_transpose_v_bf16", ptr(v), ptr(vt), b * h, s, d, stream_of(v))
 
 
-def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=64):
+def launch_factored_attention(inputs, out, inv, kn, *, causal=False, bm=64, bn=64, work=None):
     """No-RoPE factored launch (qk:641-652): ``kn = bf16(k*inv_k*gk*gq)`` and FP32
     ``inv`` ``[B,Hq,S]`` (Q's inverse RMS, applied to the scores) are written to the
     caller's buffers, then factored attention writes ``out``.  ``inputs`` uses the
     reference five-tensor order ``(q, k, v, gq, gk)``.  Returns the launched
     kernels, as ``launch_attention`` does (the reference returns its kernel
-    object, qk:651).
+    object, qk:651).  ``work``: the split-KV workspace, as for
+    ``launch_attention`` (``None`` uses the cached one when the shape splits).
     """
     q, k, v, gq, gk = inputs[:5]
     b, h, s, d = q.shape
+    wp, wb = _work_args(work, q, k.shape[1], causal)
     _lib.call("kfmi_launch_factored_attention_bf16",
               ptr(q), ptr(k), ptr(v), ptr(gq), ptr(gk), ptr(out), ptr(inv), ptr(kn),
-              b, h, k.shape[1], s, d, EPS, int(bool(causal)), _bm(bm), _bn(bn), stream_of(q))
+              b, h, k.shape[1], s, d, EPS, int(bool(causal)), _bm(bm), _bn(bn), wp, wb, stream_of(q))
     return _lib.Launches()
 
 
@@ -259,14 +261,16 @@ def prepare_factored(inputs, inv, kn):
               b, h, k.shape[1], s, d, EPS, stream_of(q))
 
 
-def factored_attention(q, kn, v, inv, out, *, causal=False, bm=64, bn=64, compute_inv=False):
+def factored_attention(q, kn, v, inv, out, *, causal=False, bm=64, bn=64, compute_inv=False, work=None):
     """The factored attention launch alone (qk:612-638) on raw ``q`` and prepared
     ``kn``; ``compute_inv=True`` derives Q's inverse RMS in the prologue (and
-    writes it to ``inv`` when given) instead of reading ``inv``."""
+    writes it to ``inv`` when given) instead of reading ``inv``.  ``work``: the
+    split-KV workspace, as for ``launch_attention``."""
     b, h, s, d = q.shape
+    wp, wb = _work_args(work, q, kn.shape[1], causal)
     _lib.call("kfmi_factored_attention_bf16", ptr(q), ptr(kn), ptr(v), ptr(inv), ptr(out),
               b, h, kn.shape[1], s, d, EPS, int(bool(causal)), int(bool(compute_inv)), _bm(bm), _bn(bn),
-              stream_of(q))
+              wp, wb, stream_of(q))
 
 
 def _bm(bm):

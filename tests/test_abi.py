@@ -91,12 +91,17 @@ CASES = [
     ("kfmi_transpose_v_bf16", (P, None, 4, 64, 128, None), "vt must not"),
     ("kfmi_factored_prepare_bf16", (P, P, P, P, None, P, 1, 16, 8, 16, 256, 1e-6, None), "inv must not"),
     ("kfmi_factored_prepare_bf16", (P, P, P, P, P, P, 1, 16, 8, 16, 256, -1.0, None), "eps"),
-    ("kfmi_factored_attention_bf16", (P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 2, 128, 64, None), "inv_mode"),
-    ("kfmi_factored_attention_bf16", (P, P, P, None, P, 1, 16, 8, 16, 256, 1e-6, 1, 0, 128, 64, None),
+    ("kfmi_factored_attention_bf16", (P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 2, 128, 64, None, 0, None), "inv_mode"),
+    ("kfmi_factored_attention_bf16", (P, P, P, None, P, 1, 16, 8, 16, 256, 1e-6, 1, 0, 128, 64, None, 0, None),
      "inv must not"),
-    ("kfmi_factored_attention_bf16", (P, P, P, P + 2, P, 1, 16, 8, 16, 256, 1e-6, 1, 1, 128, 64, None), "4-byte"),
-    ("kfmi_launch_factored_attention_bf16", (P, P, P, P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 128, 16, None),
+    ("kfmi_factored_attention_bf16", (P, P, P, P + 2, P, 1, 16, 8, 16, 256, 1e-6, 1, 1, 128, 64, None, 0, None),
+     "4-byte"),
+    ("kfmi_launch_factored_attention_bf16", (P, P, P, P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 128, 16, None, 0, None),
      "bn"),
+    ("kfmi_launch_factored_attention_bf16", (P, P, P, P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 128, 64, None, -1,
+                                             None), "work_bytes"),
+    ("kfmi_factored_attention_bf16", (P, P, P, P, P, 1, 16, 8, 16, 256, 1e-6, 1, 1, 128, 64, P + 8, 4096, None),
+     "16-byte"),
 ]
 
 

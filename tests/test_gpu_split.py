@@ -184,3 +184,39 @@ def test_captured_split_keeps_its_workspace(gpu):
         assert torch.equal(again, split), i
     ref = oracle.oracle_rows_fp32(*[t.cpu() for t in large.astuple()], torch.arange(1528, 1536), True)
     assert oracle.attention_gate(big[:, :, 1528:].cpu(), ref)["pass"]
+
+
+@pytest.mark.parametrize("geom,b,s", [((8, 4, 256), 1, 2048), ((16, 8, 256), 1, 1536), ((4, 2, 256), 2, 1000)])
+def test_factored_split_matches_unsplit(gpu, geom, b, s):
+    """The factored no-RoPE launch (qk:641-652) on the split plan: its
+    attention launch takes the same workspace.  With the cached workspace
+    (work=None) the launch record shows the split, the output passes the
+    oracle gate on the whole tensor and lies within a few ulp of the unsplit
+    launch (an empty workspace), and INV (written by both halves of a split
+    block, the same values) equals the oracle's."""
+    from kernelfuser_amd import launch_factored_attention
+
+    hq, hkv, d = geom
+    assert attention_workspace_bytes(b, hq, hkv, s, d, True) > 0, "shape expected to split"
+    xs = make_inputs(b, s, geom, 1313, rope=False)
+    g = xs.to(gpu)
+    announce(f"factored split {geom} B={b} S={s}")
+    res = []
+    for work in (None, torch.empty(0, dtype=torch.uint8, device=gpu)):
+        out = torch.full_like(g.q, float("nan"))
+        inv = torch.empty(g.q.shape[:-1], device=gpu, dtype=torch.float32)
+        kn = torch.empty_like(g.k)
+        recs = [r for r in launch_factored_attention((g.q, g.k, g.v, g.gq, g.gk), out, inv, kn, causal=True, work=work)
+                if r["kernel"].startswith("attn_")]
+        res.append((out, inv, recs[0]["plan"]))
+    torch.cuda.synchronize()
+    (split, inv_s, plan_s), (unsplit, inv_u, plan_u) = res
+    assert not plan_s.startswith("split=0") and plan_u.startswith("split=0"), (plan_s, plan_u)
+    ref = oracle.refinement_oracle_norope(xs.q, xs.k, xs.v, xs.gq, xs.gk, True, head_chunk=8)
+    m = oracle.attention_gate(split.cpu(), ref)
+    assert m["pass"], m
+    d_ = (split.float() - unsplit.float()).abs()
+    tol = 4 * bf16_ulp(torch.maximum(split.float().abs(), unsplit.float().abs())) + 1e-3
+    assert bool((d_ <= tol).all()), float((d_ / tol).max())
+    inv_ref = oracle.rms_inverse(xs.q.float())[..., 0]
+    assert torch.equal(inv_s, inv_u) and torch.allclose(inv_s.cpu(), inv_ref, rtol=1e-6, atol=0)
