@@ -10,8 +10,9 @@ the rounding style, RoPE on or off, and the attention kernel (by shape, or
 forced to each kernel the geometry admits).  Draws: 40 short cases (B in
 1..3, S from 1 to 700: one-tile items, partial tiles) and 30 long ones (B in
 1..2, S from 777 to 4096: the dispatch thresholds, the persistent pairing, the
-D=256 split plans), plus 20 short cases on geometries beyond the reference's
-table (MHA and odd GQA ratios, general kernel only).  The case lists depend
+D=256 split plans), 20 short cases on geometries beyond the reference's
+table (MHA and odd GQA ratios, general kernel only), and 16 D=256 causal
+shapes with few heads, where the general kernel splits key ranges.  The case lists depend
 only on the seeds, so every run checks the same cases.  Each test names its case before the GPU step and
 checks from the launch records that a forced kernel ran.
 """
@@ -76,8 +77,35 @@ def test_sweep_off_table_case_whole_output(gpu, name, b, s, causal, path, style,
     _check_case(gpu, name, b, s, causal, path, style, rope, kernel)
 
 
+def _split_cases(n=16, seed=7373):
+    rng = random.Random(seed)
+    geoms = [(2, 1, 256), (4, 4, 256), (6, 2, 256), (8, 4, 256), (16, 8, 256), (4, 2, 256)]
+    cases = []
+    for i in range(n):
+        geom = rng.choice(geoms)
+        b = rng.choice([1, 1, 2])
+        s = rng.randint(129, 2100)
+        path = rng.choice(["query", "query", "unfused", "factored"])
+        style = "factored" if path == "factored" else rng.choice(["fp32", "hf", "legacy"])
+        rope = path != "factored"
+        cases.append(pytest.param(geom, b, s, path, style, rope, id=f"{i:02d}-{geom[0]}q{geom[1]}kv-B{b}-S{s}-{path}-{style}"))
+    return cases
+
+
+@pytest.mark.parametrize("geom,b,s,path,style,rope", _split_cases())
+def test_sweep_split_plan_whole_output(gpu, geom, b, s, path, style, rope):
+    """D=256 causal grids with fewer query blocks than CUs: the general
+    kernel cuts its longest blocks' key ranges in two and merges the halves
+    (split-KV).  The launch record must show a split exactly when the shape
+    has a workspace, and the whole output must pass the oracle's gate."""
+    from kernelfuser_amd import attention_workspace_bytes
+    recs = _check_case(gpu, geom, b, s, True, path, style, rope, "auto")
+    n_split = int(recs[0]["plan"].split()[0].split("=")[1])
+    assert (n_split > 0) == (attention_workspace_bytes(b, geom[0], geom[1], s, 256, True) > 0), recs[0]
+
+
 def _check_case(gpu, name, b, s, causal, path, style, rope, kernel):
-    geom = GEOMETRIES[name]
+    geom = GEOMETRIES[name] if isinstance(name, str) else name
     xs = make_inputs(b, s, geom, 5000 + 7 * s + b, rope=rope)
     g = xs.to(gpu)
     out = torch.full_like(g.q, float("nan"))
@@ -92,7 +120,8 @@ def _check_case(gpu, name, b, s, causal, path, style, rope, kernel):
             recs = list(launch_attention(g.reference7, out, causal=causal, mode=path, rope=rope, qn=qn, kn=kn,
                                          norm_style=style))
     torch.cuda.synchronize()
-    attn = [r["kernel"] for r in recs if r["kernel"].startswith("attn_")]
+    attn_recs = [r for r in recs if r["kernel"].startswith("attn_")]
+    attn = [r["kernel"] for r in attn_recs]
     assert len(attn) == 1, recs
     if kernel != "auto":
         assert attn[0].startswith(KERNEL_PREFIX[kernel]), attn
@@ -105,3 +134,4 @@ def _check_case(gpu, name, b, s, causal, path, style, rope, kernel):
     gate = oracle.metric if style in ("hf", "legacy") else oracle.attention_gate
     m = gate(out.cpu(), ref)
     assert m["pass"], m
+    return attn_recs
